@@ -1,0 +1,221 @@
+"""Benchmark of the MI355X W4A8 engine on the Llama-3.2-1B decode GEMV chain.
+
+    python bench.py [--gpus 1] [--steps 400] [--warmup 20] [--no-cpu]
+
+One step = one token's 65 W4A8 GEMVs (16 x q|k|v 3072x2048, o 2048x2048,
+gate|up 16384x2048, down 2048x8192, then the LM head 128256x2048), each
+preceded by the Q8_0 quantization of a float32 activation, in order, with
+weights (695,107,584 bytes of Q4_0) resident in HBM. The chain alone is
+larger than the 256 MB Infinity Cache, so every step streams from HBM.
+
+Prints one JSON line: chain tokens/s (value), the roofline of the chain
+kernel, per-GEMV microseconds and GB/s at each layer shape and at the LM head
+(weights rotated past the Infinity Cache), and the CPU baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "llm-kv260_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+ROTATE_BYTES = 512 << 20       # >= 2 x the 256 MB Infinity Cache
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def device_weights(torch, kv, m):
+    """Q4_0 blocks of an N(0, 0.02) fp32 matrix drawn with the device RNG (seeded by
+    the matrix's weight seed) and quantized by the engine's own Q4_0 kernel."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m.w_seed)
+    w = torch.randn((m.rows, m.k), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    blocks = kv.quantize_q4_0(w)
+    del w
+    return blocks
+
+
+def build_chain(torch, kv, cf):
+    import ctypes
+
+    class CStep(ctypes.Structure):
+        _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                    ("rows", ctypes.c_int), ("k", ctypes.c_int)]
+
+    chain = cf.decode_chain()
+    mats, xs, ys = [], [], []
+    for i, m in enumerate(chain):
+        mats.append(device_weights(torch, kv, m))
+        xs.append(torch.from_numpy(cf.activation(m)).cuda())
+        ys.append(torch.empty(m.rows, dtype=torch.float32, device="cuda"))
+        if i % 16 == 15:
+            log(f"chain weights: {i + 1}/{len(chain)} matrices")
+    steps = (CStep * len(chain))(*[CStep(mats[i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), m.rows, m.k)
+                                   for i, m in enumerate(chain)])
+    torch.cuda.synchronize()
+    return chain, mats, xs, ys, steps
+
+
+def time_chain(torch, kv, steps, n, n_steps, warmup):
+    import ctypes
+    L = kv.lib()
+    ptr = ctypes.cast(steps, ctypes.c_void_p)
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(warmup):
+        kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, stream))
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(n_steps):
+        kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, stream))
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / n_steps, wall
+
+
+def time_gemv(torch, kv, cf, m, reps_min=200):
+    """us per GEMV (engine-layout x) over rotating copies of one matrix, >= 512 MB in total."""
+    base = device_weights(torch, kv, m)
+    copies = max(3, -(-ROTATE_BYTES // m.weight_bytes))
+    if m.rows * m.k >= 128256 * 2048:
+        copies = 3
+    mats = [base] + [base.clone() for _ in range(copies - 1)]
+    x = kv.quantize_q8_0_engine(torch.from_numpy(cf.activation(m)).cuda())
+    y = torch.empty(m.rows, dtype=torch.float32, device="cuda")
+    reps = max(reps_min, copies * 2)
+    for i in range(copies):                              # warm-up
+        kv.gemv_engine(mats[i], m.k, x, out=y)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for r in range(reps):
+        kv.gemv_engine(mats[r % copies], m.k, x, out=y)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / reps
+    del mats
+    return {"shape": f"{m.rows}x{m.k}", "us": round(us, 3),
+            "gbps": round(m.algorithmic_bytes / us / 1e3, 1),
+            "weight_copies": copies, "rotated_mb": round(copies * m.weight_bytes / 2**20, 1)}
+
+
+def cpu_baseline(kv, torch, chain, mats, xs, budget_s=30.0):
+    """One decode step through the NumPy restatement of q4_0.py (1 core), and the
+    same step through the scalar C restatement with OpenMP over rows (all cores)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import c_oracle
+    import q4_0_oracle
+
+    host_w = [t.cpu().numpy() for t in mats]
+    host_x = [t.cpu().numpy() for t in xs]
+    t0 = time.perf_counter()
+    for m, w, x in zip(chain, host_w, host_x):
+        xq, xd = q4_0_oracle.quantize_q8_0(x)
+        q4_0_oracle.gemv_q4_0(w, m.k, xq, xd)
+    numpy_step = time.perf_counter() - t0
+    cores = len(os.sched_getaffinity(0))
+    c_runs = []
+    for _ in range(max(1, min(5, int(budget_s / max(numpy_step, 1e-3))))):
+        t0 = time.perf_counter()
+        for m, w, x in zip(chain, host_w, host_x):
+            xq, xd = c_oracle.quantize_q8_0(x)
+            c_oracle.gemv_q4_0(w, m.k, xq, xd, threads=cores)
+        c_runs.append(time.perf_counter() - t0)
+    c_step = float(np.median(c_runs))
+    return {
+        "value": round(1.0 / numpy_step, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+        "sample": "1 decode step (65 GEMVs incl. LM head, 695 MB of Q4_0) through the NumPy "
+                  "restatement of src/llm_kv260/q4_0.py (quantize_q8_0 + gemv_q4_0 per matrix), "
+                  f"{numpy_step:.2f} s",
+        "c_openmp": {"value": round(1.0 / c_step, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+                     "sample": f"median of {len(c_runs)} decode steps through the scalar C restatement, "
+                               f"OpenMP over rows, {c_step * 1e3:.1f} ms/step"},
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the per-GEMV measurements")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this engine runs every matrix unsplit on one GPU; --gpus {args.gpus} is not "
+              "supported (the multi-GPU layout is a design note, not a build)", file=sys.stderr)
+        return 2
+
+    import torch
+    import kv260gemv as kv
+    from kv260gemv import configs as cf
+
+    kv.require_device(0)
+    torch.cuda.set_device(0)
+    log("building the 65-matrix decode chain on the device")
+    chain, mats, xs, ys, steps = build_chain(torch, kv, cf)
+    n = len(chain)
+    chain_bytes = cf.chain_algorithmic_bytes()
+    log(f"timing {args.steps} steps after {args.warmup} warm-up steps")
+    ms_per_step, wall = time_chain(torch, kv, steps, n, args.steps, args.warmup)
+    tok_s = 1e3 / ms_per_step
+    achieved = chain_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"chain: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {achieved:.0f} GB/s")
+
+    gemv = {}
+    if not args.no_gemv:
+        for m in (cf.O_PROJ,) + cf.LAYER_SHAPES + (cf.LM_HEAD,):
+            r = time_gemv(torch, kv, cf, m)
+            gemv[m.name if m is not cf.O_PROJ else "o_proj_config0"] = r
+            log(f"gemv {m.name} {r['shape']}: {r['us']} us, {r['gbps']} GB/s")
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (bounded sample)")
+        cpu = cpu_baseline(kv, torch, chain, mats, xs)
+
+    out = {
+        "metric": "1B-shape decode GEMV-chain tokens/s (W4A8 Q4_0 x Q8_0, 65 GEMVs per token)",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xint8->int32, fp32 epilogue",
+        "data": "synthetic: Q4_0 weights from N(0,0.02) drawn with the device RNG per matrix seed and "
+                "quantized by the engine; fp32 N(0,1) activations, numpy-seeded per matrix",
+        "config": {"workload": "llama-3.2-1b decode GEMV chain: 16 x (qkv 3072x2048, o 2048x2048, "
+                               "gate_up 16384x2048, down 2048x8192) + lm_head 128256x2048, M=1, "
+                               "activation re-quantized to Q8_0 before every matrix",
+                   "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
+                   "algorithmic_bytes_per_step": chain_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode step (65 fused quantize+GEMV launches)",
+                     "bytes_per_launch": chain_bytes},
+        "gemv": gemv,
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

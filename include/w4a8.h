@@ -1,0 +1,120 @@
+/*
+ * w4a8.h -- native C ABI of the MI355X W4A8 engine (libkv260gemv.so).
+ *
+ * y = W x with W in ggml Q4_0 (18-byte blocks: fp16 scale d little-endian,
+ * then 16 bytes whose byte j holds weight j in the low nibble and weight j+16
+ * in the high nibble, value (n - 8) * d) and x in Q8_0, computed byte-for-byte
+ * in the order src/llm_kv260/q4_0.py:151-182 fixes: exact int32 block dots,
+ * t = (f32(sumi) * f32(d_w)) * f32(d_x), eight fp32 lanes accumulated in block
+ * order, adjacent-pair tree.
+ *
+ * Every pointer argument is a device address (HBM; hipMalloc, torch, or the
+ * udmabuf pools of udmabuf.h). `stream` is a hipStream_t (NULL = the null
+ * stream of the current device). Calls enqueue work and return; nothing is
+ * allocated per call. Shapes and alignment are checked before anything is
+ * enqueued; a failed check returns a negative status and enqueues nothing.
+ *
+ * Shape rules: k % 256 == 0 (whole 8-block lane groups, q4_0.py:166-167),
+ * 256 <= k <= 16384, rows >= 1. Alignment: W and x 16 bytes (the engine's
+ * 16-byte vector loads; ggml and GGUF align tensor data to 32), y 4 bytes.
+ */
+#ifndef W4A8_H
+#define W4A8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A8_QK 32
+#define W4A8_Q4_0_BYTES 18
+#define W4A8_Q8_0_BYTES 34
+#define W4A8_LANES 8
+#define W4A8_MAX_K 16384
+
+enum w4a8_status {
+    W4A8_OK = 0,
+    W4A8_ERR_NULL = -1,    /* a required pointer is NULL */
+    W4A8_ERR_SHAPE = -2,   /* k or rows (or m) outside the rules above */
+    W4A8_ERR_ALIGN = -3,   /* a pointer is not aligned as required */
+    W4A8_ERR_HIP = -4,     /* the HIP runtime reported an error (w4a8_last_hip_error) */
+    W4A8_ERR_NODEV = -5,   /* no usable gfx950 device */
+};
+
+/* "llm-kv260/w4a8-q4_0-v2": the contract these kernels are held to
+ * (replaces CONTRACT_VERSION, src/llm_kv260/q4_0.py:64). */
+const char *w4a8_contract_version(void);
+const char *w4a8_strerror(int status);
+/* The hipError_t value behind the last W4A8_ERR_HIP of this thread. */
+int w4a8_last_hip_error(void);
+
+/* Bytes of one Q4_0 row, of one engine-layout activation (int8[k] then
+ * float32[k/32]) and of one row of Q8_0 blocks. */
+size_t w4a8_q4_0_row_bytes(int k);
+size_t w4a8_engine_x_bytes(int k);
+size_t w4a8_q8_0_row_bytes(int k);
+
+/* y[rows] = W[rows, k] x, x in the engine layout int8[k] | float32[k/32]
+ * (pack_x_for_engine, src/llm_kv260/q4_0.py:193-200). The call the v1 engine
+ * made with gemv_dev_run (board/kv260gemv/gemv_dev.h:19-23), now with the
+ * north-star argument order gemv(weights, activation, out, rows, cols). */
+int w4a8_gemv(const void *w, const void *x, float *y, int rows, int k, void *stream);
+
+/* Same, x as ggml Q8_0 blocks (34 bytes each: fp16 d then 32 int8). x needs
+ * only 2-byte alignment. */
+int w4a8_gemv_q8_0(const void *w, const void *x_blocks, float *y, int rows, int k, void *stream);
+
+/* Same, x as float32[k], quantized to Q8_0 inside the GEMV kernel
+ * (gemv_q4_0_f32, src/llm_kv260/q4_0.py:185-188). */
+int w4a8_gemv_f32(const void *w, const float *x, float *y, int rows, int k, void *stream);
+
+/* Four row quarters at their own addresses, rows/4 contiguous rows each,
+ * y contiguous (gemv_dev_start4, board/kv260gemv/gemv_dev.h:29-35). rows % 4 == 0. */
+int w4a8_gemv_quarters(const void *const w[4], const void *x, float *y, int rows, int k, void *stream);
+
+/* Fused Q8_0 activation quantizer (q4_0.py:83-97; the caller's quantize_x,
+ * board/tp/tp_llama.cpp:330-352): m rows of float32[k] -> m rows of the engine
+ * layout (row stride w4a8_engine_x_bytes(k)). x and out 16-byte aligned. */
+int w4a8_quantize_q8_0(const float *x, void *out_engine, int k, int m, void *stream);
+
+/* Same quantizer, output as ggml Q8_0 blocks (row stride w4a8_q8_0_row_bytes(k)). */
+int w4a8_quantize_q8_0_blocks(const float *x, void *out_blocks, int k, int m, void *stream);
+
+/* Q4_0 weight quantizer (quantize_q4_0, src/llm_kv260/q4_0.py:100-121):
+ * float32[rows][k] -> Q4_0 rows. For building matrices on the device. */
+int w4a8_quantize_q4_0(const float *w, void *out_blocks, int rows, int k, void *stream);
+
+/* Batched M > 1 (prefill): y[m][rows] = W x_i for m activation rows, each
+ * byte-identical to w4a8_gemv on that row alone. x rows in the engine layout,
+ * stride w4a8_engine_x_bytes(k). 1 <= m <= 4096. Int8 MFMA with exact
+ * per-block int32 sums, then the same fp32 epilogue per (row, token). */
+int w4a8_gemm(const void *w, const void *x_rows, float *y, int m, int rows, int k, void *stream);
+
+/* One matrix of a decode step's GEMV chain: y = W x with x given as
+ * float32[k] and quantized to Q8_0 inside the engine right before the GEMV. */
+typedef struct w4a8_chain_step {
+    const void *w;     /* Q4_0 rows, 16-byte aligned */
+    const float *x;    /* float32[k], 16-byte aligned */
+    float *y;          /* float32[rows] */
+    int rows;
+    int k;
+} w4a8_chain_step;
+
+#define W4A8_CHAIN_MAX_STEPS 96
+
+/* A token's matrices in order (board/tp/tp_llama.cpp:822-883: per layer
+ * q|k|v, o, gate|up, down, then the LM head; 65 engine calls per token).
+ * Step j does not start its dot products before step j-1's output is
+ * complete, as when x_j is computed from y_{j-1}; weights of later steps may
+ * stream earlier (the gemv2 engine's prefetch of the next matrix,
+ * board/kv260gemv/gemv2_dev.h:40-44). Each step equals w4a8_gemv_f32 on its
+ * own, byte for byte. 1 <= n <= W4A8_CHAIN_MAX_STEPS. */
+int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A8_H */

@@ -1,0 +1,135 @@
+// The native C ABI (include/w4a8.h): argument checks, then one enqueue.
+#include <stdint.h>
+
+#include "../../include/w4a8.h"
+#include "kernels.h"
+
+using namespace w4a8;
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return W4A8_OK;
+    g_last_hip_error = (int)e;
+    return W4A8_ERR_HIP;
+}
+
+bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int check_k(int k) {
+    if (k < 256 || k > W4A8_MAX_K || k % 256) return W4A8_ERR_SHAPE;
+    return W4A8_OK;
+}
+
+int check_gemv(const void *w, const void *x, const float *y, int rows, int k, uintptr_t x_align) {
+    if (!w || !x || !y) return W4A8_ERR_NULL;
+    if (check_k(k) || rows < 1) return W4A8_ERR_SHAPE;
+    if (!aligned(w, 16) || !aligned(x, x_align) || !aligned(y, 4)) return W4A8_ERR_ALIGN;
+    return W4A8_OK;
+}
+
+MatrixRef plain_matrix(const void *w, int rows, int k) {
+    MatrixRef m{};
+    m.seg[0] = static_cast<const uint8_t *>(w);
+    m.nseg = 1;
+    m.seg_rows = rows;
+    m.rows = rows;
+    m.k = k;
+    return m;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *w4a8_contract_version(void) { return "llm-kv260/w4a8-q4_0-v2"; }
+
+const char *w4a8_strerror(int status) {
+    switch (status) {
+        case W4A8_OK: return "ok";
+        case W4A8_ERR_NULL: return "a required pointer is NULL";
+        case W4A8_ERR_SHAPE: return "shape outside the engine's rules (k % 256 == 0, 256 <= k <= 16384, rows >= 1)";
+        case W4A8_ERR_ALIGN: return "pointer not aligned (weights and activations 16 B, output 4 B)";
+        case W4A8_ERR_HIP: return "HIP runtime error";
+        case W4A8_ERR_NODEV: return "no usable gfx950 device";
+        default: return "unknown status";
+    }
+}
+
+int w4a8_last_hip_error(void) { return g_last_hip_error; }
+
+size_t w4a8_q4_0_row_bytes(int k) { return k > 0 ? (size_t)k / 32 * 18 : 0; }
+size_t w4a8_engine_x_bytes(int k) { return k > 0 ? (size_t)k + (size_t)k / 32 * 4 : 0; }
+size_t w4a8_q8_0_row_bytes(int k) { return k > 0 ? (size_t)k / 32 * 34 : 0; }
+
+int w4a8_gemv(const void *w, const void *x, float *y, int rows, int k, void *stream) {
+    if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_ENGINE, y, (hipStream_t)stream));
+}
+
+int w4a8_gemv_q8_0(const void *w, const void *x_blocks, float *y, int rows, int k, void *stream) {
+    if (int s = check_gemv(w, x_blocks, y, rows, k, 2)) return s;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x_blocks, X_Q8_0, y, (hipStream_t)stream));
+}
+
+int w4a8_gemv_f32(const void *w, const float *x, float *y, int rows, int k, void *stream) {
+    if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream));
+}
+
+int w4a8_gemv_quarters(const void *const w[4], const void *x, float *y, int rows, int k, void *stream) {
+    if (!w) return W4A8_ERR_NULL;
+    for (int q = 0; q < 4; ++q) {
+        if (!w[q]) return W4A8_ERR_NULL;
+        if (!aligned(w[q], 16)) return W4A8_ERR_ALIGN;
+    }
+    if (rows % 4) return W4A8_ERR_SHAPE;
+    if (int s = check_gemv(w[0], x, y, rows, k, 16)) return s;
+    MatrixRef m{};
+    for (int q = 0; q < 4; ++q) m.seg[q] = static_cast<const uint8_t *>(w[q]);
+    m.nseg = 4;
+    m.seg_rows = rows / 4;
+    m.rows = rows;
+    m.k = k;
+    return hip_status(launch_gemv_m1(m, x, X_ENGINE, y, (hipStream_t)stream));
+}
+
+int w4a8_quantize_q8_0(const float *x, void *out_engine, int k, int m, void *stream) {
+    if (!x || !out_engine) return W4A8_ERR_NULL;
+    if (check_k(k) || m < 1) return W4A8_ERR_SHAPE;
+    if (!aligned(x, 16) || !aligned(out_engine, 16)) return W4A8_ERR_ALIGN;
+    return hip_status(launch_quantize_q8_0(x, k, m, static_cast<uint8_t *>(out_engine), X_ENGINE, (hipStream_t)stream));
+}
+
+int w4a8_quantize_q8_0_blocks(const float *x, void *out_blocks, int k, int m, void *stream) {
+    if (!x || !out_blocks) return W4A8_ERR_NULL;
+    if (check_k(k) || m < 1) return W4A8_ERR_SHAPE;
+    if (!aligned(x, 16) || !aligned(out_blocks, 2)) return W4A8_ERR_ALIGN;
+    return hip_status(launch_quantize_q8_0(x, k, m, static_cast<uint8_t *>(out_blocks), X_Q8_0, (hipStream_t)stream));
+}
+
+int w4a8_quantize_q4_0(const float *w, void *out_blocks, int rows, int k, void *stream) {
+    if (!w || !out_blocks) return W4A8_ERR_NULL;
+    if (k < 32 || k % 32 || rows < 1) return W4A8_ERR_SHAPE;
+    if (!aligned(w, 16) || !aligned(out_blocks, 2)) return W4A8_ERR_ALIGN;
+    return hip_status(launch_quantize_q4_0(w, rows, k, static_cast<uint8_t *>(out_blocks), (hipStream_t)stream));
+}
+
+int w4a8_gemm(const void *w, const void *x_rows, float *y, int m, int rows, int k, void *stream) {
+    if (int s = check_gemv(w, x_rows, y, rows, k, 16)) return s;
+    if (m < 1 || m > 4096) return W4A8_ERR_SHAPE;
+    return hip_status(launch_gemm(plain_matrix(w, rows, k), static_cast<const uint8_t *>(x_rows), m, y,
+                                  (hipStream_t)stream));
+}
+
+int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream) {
+    if (!steps) return W4A8_ERR_NULL;
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
+    for (int i = 0; i < n; ++i)
+        if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
+    return hip_status(launch_chain(steps, n, (hipStream_t)stream));
+}
+
+}  // extern "C"

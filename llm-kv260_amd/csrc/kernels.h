@@ -1,0 +1,59 @@
+// Host-side launchers of the engine's HIP kernels (internal to the library).
+// Argument checking happens in the C ABI layer (api.cpp); these assume valid,
+// already-checked shapes and pointers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a8 {
+
+// Activation formats the GEMV kernels can stage.
+enum XFormat : int {
+    X_ENGINE = 0,   // int8[K] then float32[K/32]  (pack_x_for_engine, q4_0.py:193-200)
+    X_Q8_0 = 1,     // ggml Q8_0 blocks: fp16 d then 32 int8, 34 bytes each
+    X_F32 = 2,      // float32[K], quantized to Q8_0 inside the kernel (fused)
+};
+
+// Up to four row segments of one matrix: rows [s*seg_rows, (s+1)*seg_rows) live
+// contiguously (row-major, K/32*18 bytes per row) from seg[s]. One segment is a
+// plain ggml matrix; four are the reference v1 engine's per-engine quarters.
+// Output rows are contiguous: y[s*seg_rows + r].
+// paired: the v2 engine's port layout instead -- in a segment of R rows, row i
+// and row i + R/2 form a pair whose 144-byte chunks alternate
+// (board/kv260gemv/gemv2_dev.h:46-49, 66-72); R must be even.
+struct MatrixRef {
+    const uint8_t *seg[4];
+    int nseg;
+    int seg_rows;
+    int rows;
+    int k;
+    bool paired;
+};
+
+constexpr int MAX_K_M1 = 16384;   // LDS-staged activation limit of the M=1 kernel
+constexpr int MAX_K_GEMM = 16384;
+
+int device_cu_count();            // of the current device (cached per device)
+
+hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream);
+
+// y[m][rows] for m activation rows in engine layout (row stride K + K/8 bytes).
+hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, float *y, hipStream_t stream);
+
+// x: float32[m][K] -> engine layout rows, or ggml Q8_0 block rows.
+hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFormat out_fmt, hipStream_t stream);
+
+}  // namespace w4a8
+
+struct w4a8_chain_step;   // include/w4a8.h
+
+namespace w4a8 {
+
+// The decode chain: one GEMV per step, in order, x quantized inside.
+hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream);
+
+// w: float32[rows][K] -> Q4_0 rows.
+hipError_t launch_quantize_q4_0(const float *w, int rows, int k, uint8_t *out, hipStream_t stream);
+
+}  // namespace w4a8

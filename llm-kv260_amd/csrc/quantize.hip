@@ -1,0 +1,123 @@
+// Quantizer kernels: the fused Q8_0 activation quantizer (the engine caller's
+// quantize_x, board/tp/tp_llama.cpp:330-352, with the contract's rounding,
+// src/llm_kv260/q4_0.py:83-97) and a Q4_0 weight quantizer
+// (src/llm_kv260/q4_0.py:100-121) for building matrices on the device.
+//
+// Both are element-wise over 32-element blocks: one thread per block, 32
+// floats in through eight 16-byte loads. They are tiny next to the GEMV
+// (K floats per activation; weights are quantized once).
+#include "kernels.h"
+#include "q4_0_device.h"
+
+namespace w4a8 {
+
+namespace {
+
+__device__ __forceinline__ void load_block(const float *src, float v[32]) {
+    const float4 *p = reinterpret_cast<const float4 *>(src);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const float4 f = p[m];
+        v[4 * m] = f.x; v[4 * m + 1] = f.y; v[4 * m + 2] = f.z; v[4 * m + 3] = f.w;
+    }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int k, int m,
+                                                            uint8_t *__restrict__ out) {
+    const int nb = k >> 5;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long)nb * m) return;
+    const int row = (int)(gid / nb), b = (int)(gid - (long)row * nb);
+    float v[32];
+    load_block(x + (size_t)row * k + 32 * b, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    const float d = q8_scale(amax);
+    const float inv = safe_recip(d);
+    uint32_t q[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) word |= ((uint32_t)(uint8_t)q8_round(v[4 * w + e], inv)) << (8 * e);
+        q[w] = word;
+    }
+    const uint16_t dh = float_to_half_bits(d);
+    if constexpr (OUT == X_ENGINE) {
+        uint8_t *rowp = out + (size_t)row * (k + 4 * nb);
+        uint4 *dst = reinterpret_cast<uint4 *>(rowp + 32 * b);
+        dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+        dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+        reinterpret_cast<float *>(rowp + k)[b] = half_bits_to_float(dh);
+    } else {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(out + ((size_t)row * nb + b) * Q8_0_BYTES);
+        dst[0] = dh;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            dst[1 + 2 * w] = (uint16_t)(q[w] & 0xFFFFu);
+            dst[2 + 2 * w] = (uint16_t)(q[w] >> 16);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void quantize_q4_0_kernel(const float *__restrict__ w, int rows, int k,
+                                                            uint8_t *__restrict__ out) {
+    const int nb = k >> 5;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long)nb * rows) return;
+    float v[32];
+    load_block(w + gid * 32, v);   // rows are contiguous: block gid starts at float 32 * gid
+    // The signed element of largest magnitude, first index on ties.
+    float extreme = v[0], amax = fabsf(v[0]);
+#pragma unroll
+    for (int e = 1; e < 32; ++e) {
+        const float a = fabsf(v[e]);
+        if (a > amax) { amax = a; extreme = v[e]; }
+    }
+    const float d = extreme / -8.0f;
+    const float inv = safe_recip(d);
+    uint32_t nib[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        const float s = v[e] * inv;
+        const float u = s + 8.5f;
+        const int n = (int)truncf(u);   // u >= 0.5 for every finite block; clamp keeps nibbles 4-bit
+        nib[e] = (uint32_t)(n > 15 ? 15 : (n < 0 ? 0 : n));
+    }
+    uint16_t *dst = reinterpret_cast<uint16_t *>(out + gid * Q4_0_BYTES);
+    dst[0] = float_to_half_bits(d);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t b0 = nib[2 * j] | (nib[2 * j + 16] << 4);
+        const uint32_t b1 = nib[2 * j + 1] | (nib[2 * j + 17] << 4);
+        dst[1 + j] = (uint16_t)(b0 | (b1 << 8));
+    }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFormat out_fmt, hipStream_t stream) {
+    const long blocks = (long)(k / 32) * m;
+    if (blocks == 0) return hipSuccess;
+    const int grid = (int)((blocks + 255) / 256);
+    if (out_fmt == X_ENGINE)
+        hipLaunchKernelGGL(quantize_q8_0_kernel<X_ENGINE>, dim3(grid), dim3(256), 0, stream, x, k, m, out);
+    else if (out_fmt == X_Q8_0)
+        hipLaunchKernelGGL(quantize_q8_0_kernel<X_Q8_0>, dim3(grid), dim3(256), 0, stream, x, k, m, out);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q4_0(const float *w, int rows, int k, uint8_t *out, hipStream_t stream) {
+    const long blocks = (long)(k / 32) * rows;
+    if (blocks == 0) return hipSuccess;
+    const long grid = (blocks + 255) / 256;
+    if (grid > 0x7fffffffL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(quantize_q4_0_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, rows, k, out);
+    return hipGetLastError();
+}
+
+}  // namespace w4a8
