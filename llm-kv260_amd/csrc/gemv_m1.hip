@@ -1,28 +1,36 @@
 // M = 1 W4A8 GEMV for gfx950: y[N] = W[N, K] x, W in ggml Q4_0, x in Q8_0.
 //
-// A bandwidth problem with a latency tail, so no MFMA and no barriers in the
-// row loop. The unit of work is a row and the unit of parallelism a wave64:
+// A bandwidth problem with a latency tail, so no MFMA. What bounds it is how
+// many weight bytes each CU keeps in flight (HBM3E needs ~150 KB per CU to
+// run near its plateau) and how cleanly they stream, so the kernel is built
+// around wide, fully coalesced, non-temporal loads held in registers:
 //
-//  * Lane j of a wave owns block j of the row (and j + 64, j + 128, ... when
-//    K/32 > 64; several rows share a wave when K/32 < 64). Consecutive lanes
-//    own consecutive 18-byte blocks, so the wave's five dword loads per block
-//    cover the row's bytes contiguously: coalesced without any staging. An
-//    18-byte block starts 0 or 2 bytes into a dword (even / odd block), so one
-//    v_perm_b32 per nibble dword, with a per-lane selector, realigns it.
+//  * The unit of work is a chunk: eight consecutive blocks of a row, 144
+//    bytes, i.e. nine 16-byte pieces (the 9-beat chunk hls/int4_core/q4_0.h:
+//    21-25 streams). A wave tile is 64 / C whole rows (C = K / 256 chunks per
+//    row), at most 64 chunks = 9,216 contiguous bytes: nine
+//    global_load_dwordx4, lane l loading bytes 1024 p + 16 l of the tile.
+//  * Each wave keeps three tiles in registers: while it computes one, the
+//    next two are in flight, and the one it just consumed is refilled before
+//    its terms are computed (27 KB per wave, 8 waves per CU).
+//  * A tile's pieces go through a per-wave 9 KB LDS slab (ds_write_b128 in
+//    load order, ds_read_b128 in chunk order), so that lane l ends up with
+//    chunk l: 144 bytes, eight whole blocks.
+//  * Lane l owns chunk column c = l % C of the tile's rows. The tile is whole
+//    rows, so c never changes: the 256 int8 activations, 8 scales and 8 block
+//    sums of column c are read from LDS into registers once.
 //  * The activation is staged once per workgroup in LDS (quantized there from
-//    fp32 for the fused entry point) with each block's int8 sum, then every
-//    lane keeps its own blocks' 32 int8 values, scale and sum in registers for
-//    all the rows the wave visits.
+//    fp32 by the fused entry points); its loads are issued before the first
+//    tiles', so they do not wait behind the weights.
 //  * Each block's dot is exact in int32: eight v_dot4_i32_i8 on the unsigned
 //    nibbles minus 8 * sum(x). Then t = (f32(sumi) * d_w) * d_x.
-//  * The contract's order (src/llm_kv260/q4_0.py:170-182): lane l of a row
-//    adds the terms of blocks l, l + 8, l + 16, ... in that order. Those terms
-//    sit in lanes l, l + 8, ... of the wave (blocks j + 64m follow m-major),
-//    so each lane gathers them with ds_bpermute in block order and adds them
-//    one by one from +0.0f; the eight lane sums of a row then meet in a DPP
-//    adjacent-pair tree.
-//  * Weight loads for the wave's next row are issued before the current row is
-//    reduced, so each wave keeps two rows of loads in flight.
+//  * The contract's order (src/llm_kv260/q4_0.py:170-182): lane a of a row
+//    adds the terms of blocks a, a + 8, a + 16, ... in that order, from +0.0f.
+//    Chunk c holds terms 8c .. 8c + 7, so accumulator a needs term a of every
+//    chunk of the row, in chunk order: each lane writes its eight terms to
+//    the slab, and lane 8r + a of the wave reads term a of chunks 0 .. C-1 of
+//    row r and adds them one by one. The eight lane sums of a row then meet
+//    in a DPP adjacent-pair tree.
 #include "../../include/w4a8.h"
 #include "kernels.h"
 #include "q4_0_device.h"
@@ -31,10 +39,10 @@ namespace w4a8 {
 
 namespace {
 
-constexpr int THREADS = 256;
-constexpr int WAVES = THREADS / 64;
-constexpr int MAX_NB = MAX_K_M1 / QK;            // 512 blocks
-constexpr int MAX_NBPL = MAX_NB / 64;            // blocks per lane
+constexpr int MAX_THREADS = 512;
+constexpr size_t LDS_BUDGET = 160 * 1024;   // per CU on gfx950
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemvParams {
     const uint8_t *seg[4];
@@ -43,35 +51,84 @@ struct GemvParams {
     int seg_rows;     // rows per segment
     int nseg;
     int k;
-    int lpr;          // lanes per row: min(K/32, 64)
-    int rpw;          // rows per wave: 64 / lpr
-    int groups;       // row groups (of rpw rows) in the whole matrix
+    int rows;         // seg_rows * nseg
+    int C;            // chunks per row, k / 256
+    int rpw;          // rows per wave tile, 64 / C
+    int tiles;        // ceil(rows / rpw)
     int paired;       // v2 port layout
 };
 
-// Stage block b of the activation into LDS: int8 values, fp32 scale, int8 sum.
+// Address of chunk c of row r (r counted over the whole matrix).
+template <bool PLAIN>
+__device__ __forceinline__ const uint8_t *chunk_ptr(const GemvParams &P, int r, int c) {
+    if constexpr (PLAIN) {
+        return P.seg[0] + ((size_t)r * (size_t)P.C + (size_t)c) * CHUNK_BYTES;
+    } else {
+        const int seg = r / P.seg_rows, local = r - seg * P.seg_rows;
+        const uint8_t *base = P.seg[seg];
+        if (P.paired) {
+            // v2 port region: row i pairs with row i + R/2; their 144-byte chunks alternate.
+            const int half = P.seg_rows >> 1;
+            const int which = local >= half, i = local - which * half;
+            return base + (((size_t)i * (size_t)P.C + (size_t)c) * 2 + (size_t)which) * CHUNK_BYTES;
+        }
+        return base + ((size_t)local * (size_t)P.C + (size_t)c) * CHUNK_BYTES;
+    }
+}
+
+// Raw activation block as the global loads deliver it, before staging.
 template <int XF>
-__device__ __forceinline__ void stage_x_block(const void *x, int k, int b, uint32_t *s_q, float *s_d, int32_t *s_s) {
+struct XRaw;
+template <>
+struct XRaw<X_ENGINE> {
+    u32x4 q0, q1;
+    float d;
+};
+template <>
+struct XRaw<X_Q8_0> {
+    uint16_t h[17];
+};
+template <>
+struct XRaw<X_F32> {
+    float4 v[8];
+};
+
+template <int XF>
+__device__ __forceinline__ void x_load(const void *x, int k, int b, XRaw<XF> &r) {
+    if constexpr (XF == X_ENGINE) {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(x) + 32 * b);
+        r.q0 = src[0];
+        r.q1 = src[1];
+        r.d = reinterpret_cast<const float *>(static_cast<const uint8_t *>(x) + k)[b];
+    } else if constexpr (XF == X_Q8_0) {
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(x) + Q8_0_BYTES * b);
+#pragma unroll
+        for (int i = 0; i < 17; ++i) r.h[i] = src[i];
+    } else {
+        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + 32 * b);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) r.v[m] = src[m];
+    }
+}
+
+// Quantize (if fp32) and store block b into LDS: int8 values, fp32 scale, int8 sum.
+template <int XF>
+__device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_q, float *s_d, int32_t *s_s) {
     uint32_t q[8];
     float dx;
     if constexpr (XF == X_ENGINE) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(x) + 32 * b);
-        const uint4 a = src[0], c = src[1];
-        q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w;
-        q[4] = c.x; q[5] = c.y; q[6] = c.z; q[7] = c.w;
-        dx = reinterpret_cast<const float *>(static_cast<const uint8_t *>(x) + k)[b];
+        q[0] = r.q0.x; q[1] = r.q0.y; q[2] = r.q0.z; q[3] = r.q0.w;
+        q[4] = r.q1.x; q[5] = r.q1.y; q[6] = r.q1.z; q[7] = r.q1.w;
+        dx = r.d;
     } else if constexpr (XF == X_Q8_0) {
-        const uint16_t *src = reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(x) + Q8_0_BYTES * b);
-        dx = half_bits_to_float(src[0]);
+        dx = half_bits_to_float(r.h[0]);
 #pragma unroll
-        for (int m = 0; m < 8; ++m) q[m] = (uint32_t)src[1 + 2 * m] | ((uint32_t)src[2 + 2 * m] << 16);
+        for (int m = 0; m < 8; ++m) q[m] = (uint32_t)r.h[1 + 2 * m] | ((uint32_t)r.h[2 + 2 * m] << 16);
     } else {
-        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + 32 * b);
         float v[32];
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const float4 f = src[m];
-            v[4 * m] = f.x; v[4 * m + 1] = f.y; v[4 * m + 2] = f.z; v[4 * m + 3] = f.w;
+            v[4 * m] = r.v[m].x; v[4 * m + 1] = r.v[m].y; v[4 * m + 2] = r.v[m].z; v[4 * m + 3] = r.v[m].w;
         }
         float amax = 0.0f;
 #pragma unroll
@@ -90,160 +147,227 @@ __device__ __forceinline__ void stage_x_block(const void *x, int k, int b, uint3
     int32_t sum = 0;
 #pragma unroll
     for (int m = 0; m < 8; ++m) sum = __builtin_amdgcn_sdot4((int)q[m], 0x01010101, sum, false);
-    uint4 *dst = reinterpret_cast<uint4 *>(s_q + 8 * b);
-    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(s_q + 8 * b);
+    dst[0] = (u32x4){q[0], q[1], q[2], q[3]};
+    dst[1] = (u32x4){q[4], q[5], q[6], q[7]};
     s_d[b] = dx;
     s_s[b] = sum;
 }
 
-// Byte address of block b of row r (r counted over the whole matrix).
-__device__ __forceinline__ const uint8_t *block_addr(const GemvParams &P, int r, int b) {
-    const int nch = P.k >> 8;
-    const int seg = r / P.seg_rows, local = r - seg * P.seg_rows;
-    const uint8_t *base = P.seg[seg];
-    if (P.paired) {
-        // v2 port region: row i pairs with row i + R/2; their 144-byte chunks alternate.
-        const int half = P.seg_rows >> 1;
-        const int which = local >= half, i = local - which * half;
-        return base + ((size_t)(i * nch + (b >> 3)) * 2 + which) * CHUNK_BYTES + Q4_0_BYTES * (b & 7);
+// The eight terms of one chunk.
+__device__ __forceinline__ void chunk_terms(const uint32_t w[CHUNK_DWORDS], const uint32_t xv[8][8], const float xd[8],
+                                            const int32_t xs[8], float t[8]) {
+#define W4A8_TERM(J)                                                             \
+    {                                                                            \
+        uint32_t d_bits, qs[4];                                                  \
+        chunk_block<J>(w, d_bits, qs);                                           \
+        const int32_t sumi = block_dot_raw(qs, xv[J]) - 8 * xs[J];               \
+        t[J] = block_term(sumi, d_bits, xd[J]);                                  \
     }
-    return base + (size_t)local * (size_t)(nch * CHUNK_BYTES) + (size_t)Q4_0_BYTES * b;
+    W4A8_TERM(0) W4A8_TERM(1) W4A8_TERM(2) W4A8_TERM(3)
+    W4A8_TERM(4) W4A8_TERM(5) W4A8_TERM(6) W4A8_TERM(7)
+#undef W4A8_TERM
 }
 
-// The five dwords covering an 18-byte block (4-byte aligned start, 0 or 2 bytes early).
-struct BlockWords {
-    uint32_t w[5];
+constexpr int TILE_BYTES = 64 * CHUNK_BYTES;   // 9,216
+// Tiles per wave held in registers: three for plain matrices; two for the
+// board layouts, whose per-lane address tables take the third's registers.
+template <bool PLAIN>
+constexpr int depth_of() { return PLAIN ? 3 : 2; }
+
+struct Tile {
+    u32x4 p[CHUNK_PIECES];
 };
 
-__device__ __forceinline__ BlockWords load_block(const uint8_t *p) {
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
-    BlockWords r;
+// Load the nine pieces of `tile` (lane l: bytes 1024 p + 16 l of the tile).
+template <bool PLAIN>
+__device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lane, const int dr[9], const int col[9],
+                                          const int pc[9], Tile &t) {
+    if constexpr (PLAIN) {
+        const size_t tile_bytes = (size_t)P.rpw * (size_t)P.C * CHUNK_BYTES;
+        const size_t total = (size_t)P.rows * (size_t)P.C * CHUNK_BYTES;
+        const size_t off0 = (size_t)tile * tile_bytes;
+        const uint8_t *base = P.seg[0] + off0 + 16 * lane;
+        if (off0 + TILE_BYTES <= total) {
 #pragma unroll
-    for (int i = 0; i < 5; ++i) r.w[i] = __builtin_nontemporal_load(q + i);
-    return r;
-}
-
-// Term t of one block: odd = the block starts 2 bytes into its first dword.
-// The nibble bytes start 2 (even) or 4 (odd) bytes into the five dwords;
-// v_perm_b32 picks the four bytes of each nibble dword from the pair
-// {w[m+1], w[m]} with a per-lane selector (bytes 0-3 = w[m], 4-7 = w[m+1]).
-__device__ __forceinline__ float block_term_words(const BlockWords &bw, bool odd, const uint32_t xv[8], int32_t xsum,
-                                                  float dx) {
-    const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
-    uint32_t qs[4];
+            for (int p = 0; p < CHUNK_PIECES; ++p)
+                t.p[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + 1024 * p));
+        } else {
+            // The last tile overhangs the matrix: pieces past the end read
+            // its first bytes instead (their terms are never stored).
 #pragma unroll
-    for (int m = 0; m < 4; ++m) qs[m] = __builtin_amdgcn_perm(bw.w[m + 1], bw.w[m], sel);
-    const uint32_t d_bits = odd ? (bw.w[0] >> 16) : (bw.w[0] & 0xFFFFu);
-    const int32_t sumi = block_dot_raw(qs, xv) - 8 * xsum;
-    return block_term(sumi, d_bits, dx);
+            for (int p = 0; p < CHUNK_PIECES; ++p) {
+                const size_t off = off0 + 1024 * p + 16 * lane;
+                const uint8_t *g = off + 16 <= total ? P.seg[0] + off : P.seg[0];
+                t.p[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(g));
+            }
+        }
+    } else {
+        const int row0 = tile * P.rpw;
+#pragma unroll
+        for (int p = 0; p < CHUNK_PIECES; ++p) {
+            const int r = row0 + dr[p];
+            const uint8_t *g = (dr[p] < P.rpw && r < P.rows) ? chunk_ptr<false>(P, r, col[p]) + 16 * pc[p] : P.seg[0];
+            t.p[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(g));
+        }
+    }
 }
 
-__device__ __forceinline__ float bpermute_f(int src_lane, float v) {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int XF, int NBPL>
-__global__ __launch_bounds__(THREADS) void gemv_m1_kernel(GemvParams P) {
-    __shared__ __attribute__((aligned(16))) uint32_t s_q[MAX_NB * 8];
-    __shared__ float s_d[MAX_NB];
-    __shared__ int32_t s_s[MAX_NB];
-
+// LDS layout (dynamic): per-wave slabs [waves][9216] | x int8[K] | x scale
+// f32[nb] | x sum i32[nb].
+template <int XF, bool PLAIN>
+__global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int nb = P.k >> 5;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int nb = P.k >> 5;
-    const int total_rows = P.seg_rows * P.nseg;
+    const int wave = tid >> 6;
+    const int nthreads = blockDim.x;
+    const int waves = nthreads >> 6;
+    uint8_t *slab = lds + (size_t)wave * TILE_BYTES;
+    uint32_t *s_q = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
+    float *s_d = reinterpret_cast<float *>(s_q + 8 * nb);
+    int32_t *s_s = reinterpret_cast<int32_t *>(s_q + 9 * nb);
 
-    for (int b = tid; b < nb; b += THREADS) stage_x_block<XF>(P.x, P.k, b, s_q, s_d, s_s);
+    const int C = P.C, rpw = P.rpw;
+    const int my_r = lane / C;
+    const int my_c = lane - my_r * C;
+    const bool lane_live = my_r < rpw;
+
+    // Piece 64 p + lane of a tile: chunk q = n / 9 of the tile, piece n % 9
+    // of the chunk; the chunk is row q / C (of the tile), column q % C.
+    int dr[9], col[9], pc[9];
+    if constexpr (!PLAIN) {
+#pragma unroll
+        for (int p = 0; p < CHUNK_PIECES; ++p) {
+            const int n = 64 * p + lane, q = n / CHUNK_PIECES;
+            pc[p] = n - q * CHUNK_PIECES;
+            dr[p] = q / C;
+            col[p] = q - dr[p] * C;
+        }
+    }
+
+    constexpr int DEPTH = depth_of<PLAIN>();
+    // 1. Activation loads first, then the first DEPTH tiles.
+    XRaw<XF> xr;
+    if (tid < nb) x_load<XF>(P.x, P.k, tid, xr);
+    int tile = blockIdx.x * waves + wave;
+    const int tstride = gridDim.x * waves;
+    Tile buf[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+        if (tile + d * tstride < P.tiles) load_tile<PLAIN>(P, tile + d * tstride, lane, dr, col, pc, buf[d]);
+
+    // 2. Stage the activation, then pull this lane's chunk column into registers.
+    if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s);
+    for (int b = tid + nthreads; b < nb; b += nthreads) {
+        XRaw<XF> xb;
+        x_load<XF>(P.x, P.k, b, xb);
+        x_stage<XF>(xb, b, s_q, s_d, s_s);
+    }
     __syncthreads();
-
-    // This lane's place: row slot within the wave's row group, block column.
-    const int lpr = P.lpr;
-    const int slot = lane / lpr;
-    const int col = lane - slot * lpr;
-    const bool lane_live = slot < P.rpw;
-    const int row_lane0 = slot * lpr;        // first lane of this lane's row
-    const int l8 = lane & 7;
-
-    // The lane's activation blocks, kept in registers for every row.
-    uint32_t xv[NBPL][8];
-    float xd[NBPL];
-    int32_t xs[NBPL];
-    bool has[NBPL];
-#pragma unroll
-    for (int m = 0; m < NBPL; ++m) {
-        const int b = col + 64 * m;
-        has[m] = lane_live && b < nb;
-        const int bb = has[m] ? b : 0;
-        const uint4 *src = reinterpret_cast<const uint4 *>(s_q + 8 * bb);
-        const uint4 a = src[0], c = src[1];
-        xv[m][0] = a.x; xv[m][1] = a.y; xv[m][2] = a.z; xv[m][3] = a.w;
-        xv[m][4] = c.x; xv[m][5] = c.y; xv[m][6] = c.z; xv[m][7] = c.w;
-        xd[m] = s_d[bb];
-        xs[m] = s_s[bb];
-    }
-
-    const int wave_id = blockIdx.x * WAVES + (tid >> 6);
-    const int nwaves = gridDim.x * WAVES;
-    int g = wave_id;
-    if (g >= P.groups) return;
-
-    BlockWords cur[NBPL];
+    uint32_t xv[8][8];
+    float xd[8];
+    int32_t xs[8];
     {
-        int r = g * P.rpw + slot;
-        r = r < total_rows ? r : total_rows - 1;
+        const int cb = lane_live ? 8 * my_c : 0;
 #pragma unroll
-        for (int m = 0; m < NBPL; ++m) cur[m] = load_block(block_addr(P, r, has[m] ? col + 64 * m : 0));
+        for (int j = 0; j < 8; ++j) {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(s_q + 8 * (cb + j));
+            const u32x4 a = src[0], c = src[1];
+            xv[j][0] = a.x; xv[j][1] = a.y; xv[j][2] = a.z; xv[j][3] = a.w;
+            xv[j][4] = c.x; xv[j][5] = c.y; xv[j][6] = c.z; xv[j][7] = c.w;
+            xd[j] = s_d[cb + j];
+            xs[j] = s_s[cb + j];
+        }
     }
 
-    const int groups8 = lpr >> 3;
-    for (; g < P.groups; g += nwaves) {
-        const int r = g * P.rpw + slot;
-        const int gn = g + nwaves;
-        BlockWords nxt[NBPL];
-        if (gn < P.groups) {
-            int rn = gn * P.rpw + slot;
-            rn = rn < total_rows ? rn : total_rows - 1;
+    const int acc_r = lane >> 3, acc_a = lane & 7;
+    // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
+    // slab -> ordered lane sums -> tree -> y; then the buffer is refilled.
+    auto step = [&](Tile &b) {
+        u32x4 *wslab = reinterpret_cast<u32x4 *>(slab);
 #pragma unroll
-            for (int m = 0; m < NBPL; ++m) nxt[m] = load_block(block_addr(P, rn, has[m] ? col + 64 * m : 0));
+        for (int p = 0; p < CHUNK_PIECES; ++p) wslab[64 * p + lane] = b.p[p];
+        wave_sync_lds();
+        uint32_t w[CHUNK_DWORDS];
+        {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(slab + CHUNK_BYTES * lane);
+#pragma unroll
+            for (int q = 0; q < CHUNK_PIECES; ++q) {
+                const u32x4 v = src[q];
+                w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+            }
         }
-
-        float t[NBPL];
+        const int tn = tile + DEPTH * tstride;
+        if (tn < P.tiles) load_tile<PLAIN>(P, tn, lane, dr, col, pc, b);
+        float t[8];
+        chunk_terms(w, xv, xd, xs, t);
+        wave_sync_lds();
+        // Terms at a stride of nine floats per lane: both the writes (lane l,
+        // term j -> 9 l + j) and the ordered reads below hit distinct banks.
+        float *s_t = reinterpret_cast<float *>(slab);
 #pragma unroll
-        for (int m = 0; m < NBPL; ++m)
-            t[m] = has[m] ? block_term_words(cur[m], (col & 1) != 0, xv[m], xs[m], xd[m]) : 0.0f;
-
-        // Lane l8 of the row: terms of blocks l8, l8 + 8, ... in block order.
-        // Blocks beyond K/32 contribute +0.0f at the end of the order, which
-        // leaves a sum that started from +0.0f unchanged.
-        float acc = 0.0f;
+        for (int j = 0; j < 8; ++j) s_t[9 * lane + j] = t[j];
+        wave_sync_lds();
+        // Accumulator a of row r: term a of chunks 0 .. C-1, in order, from
+        // +0.0f. Eight rows per pass (more than one pass only when C < 8).
+        // The reads go eight at a time; a column past C contributes +0.0f,
+        // which leaves the sum unchanged (it started at +0.0f, so it is never
+        // -0.0f, and x + 0 = x for every other x).
+        for (int r = acc_r; r - acc_r < rpw; r += 8) {
+            float acc = 0.0f;
+            if (r < rpw) {
+                const float *src = s_t + r * C * 9 + acc_a;
+                for (int c0 = 0; c0 < C; c0 += 8) {
+                    float v[8];
 #pragma unroll
-        for (int m = 0; m < NBPL; ++m) {
-            for (int c8 = 0; c8 < groups8; ++c8) acc = acc + bpermute_f(row_lane0 + 8 * c8 + l8, t[m]);
+                    for (int j = 0; j < 8; ++j) v[j] = c0 + j < C ? src[9 * (c0 + j)] : 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc = acc + v[j];
+                }
+            }
+            const float yv = tree8_dpp(acc);
+            const int row = tile * rpw + r;
+            if (r < rpw && acc_a == 0 && row < P.rows) P.y[row] = yv;
         }
-        const float yv = tree8_dpp(acc);
-        if (lane_live && col == 0 && r < total_rows) P.y[r] = yv;
-
-#pragma unroll
-        for (int m = 0; m < NBPL; ++m) cur[m] = nxt[m];
+        wave_sync_lds();
+        tile += tstride;
+    };
+    while (tile < P.tiles) {
+        step(buf[0]);
+        if (tile >= P.tiles) break;
+        step(buf[1]);
+        if constexpr (DEPTH == 3) {
+            if (tile >= P.tiles) break;
+            step(buf[2]);
+        }
     }
+}
+
+template <int XF, bool PLAIN>
+hipError_t launch_xf(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
+    // Dynamic LDS above the default 64 KB must be allowed per kernel once.
+    static bool lds_allowed = false;
+    if (!lds_allowed) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BUDGET);
+        if (e != hipSuccess) return e;
+        lds_allowed = true;
+    }
+    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN>), dim3(grid), dim3(threads), lds, stream, P);
+    return hipGetLastError();
 }
 
 template <int XF>
-hipError_t launch_xf(const GemvParams &P, int nbpl, int grid, hipStream_t stream) {
-    const dim3 g(grid), b(THREADS);
-    switch (nbpl) {
-        case 1: hipLaunchKernelGGL((gemv_m1_kernel<XF, 1>), g, b, 0, stream, P); break;
-        case 2: hipLaunchKernelGGL((gemv_m1_kernel<XF, 2>), g, b, 0, stream, P); break;
-        case 3: hipLaunchKernelGGL((gemv_m1_kernel<XF, 3>), g, b, 0, stream, P); break;
-        case 4: hipLaunchKernelGGL((gemv_m1_kernel<XF, 4>), g, b, 0, stream, P); break;
-        case 5: hipLaunchKernelGGL((gemv_m1_kernel<XF, 5>), g, b, 0, stream, P); break;
-        case 6: hipLaunchKernelGGL((gemv_m1_kernel<XF, 6>), g, b, 0, stream, P); break;
-        case 7: hipLaunchKernelGGL((gemv_m1_kernel<XF, 7>), g, b, 0, stream, P); break;
-        case 8: hipLaunchKernelGGL((gemv_m1_kernel<XF, 8>), g, b, 0, stream, P); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+hipError_t launch_layout(const GemvParams &P, bool plain, int grid, int threads, size_t lds, hipStream_t stream) {
+    return plain ? launch_xf<XF, true>(P, grid, threads, lds, stream) : launch_xf<XF, false>(P, grid, threads, lds, stream);
 }
 
 }  // namespace
@@ -268,25 +392,40 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     P.seg_rows = w.seg_rows;
     P.nseg = w.nseg;
     P.k = w.k;
+    P.rows = w.seg_rows * w.nseg;
     P.paired = w.paired ? 1 : 0;
-    const int nb = w.k / QK;
-    P.lpr = nb < 64 ? nb : 64;
-    P.rpw = 64 / P.lpr;
-    const int rows = w.seg_rows * w.nseg;
-    P.groups = (rows + P.rpw - 1) / P.rpw;
-    const int nbpl = (nb + 63) / 64;
-    if (nbpl > MAX_NBPL) return hipErrorInvalidValue;
-    // Enough waves for every row group up to a few workgroups per CU; beyond
-    // that each wave walks several row groups.
+    P.C = w.k / 256;
+    if (P.C < 1 || P.C > 64 || w.k % 256) return hipErrorInvalidValue;
+    P.rpw = 64 / P.C;
+    P.tiles = (P.rows + P.rpw - 1) / P.rpw;
+    if (P.tiles < 1) return hipSuccess;
+    const bool plain = w.nseg == 1 && !w.paired;
     const int cus = device_cu_count();
-    const int per_cu = nbpl <= 2 ? 8 : 4;
-    int grid = (P.groups + WAVES - 1) / WAVES;
-    if (grid > cus * per_cu) grid = cus * per_cu;
-    if (grid < 1) return hipSuccess;
+    const int nb = w.k / QK;
+    const size_t x_lds = (size_t)nb * 40;
+    // Small matrices: one wave per workgroup and one workgroup per tile,
+    // spread over every CU (each stages its own copy of x in parallel).
+    // Larger ones: at most eight waves per CU (the register budget of three
+    // tiles per wave allows two waves per SIMD), every wave walking tiles
+    // with a stride of the whole grid.
+    int waves = 1;
+    int grid = P.tiles;
+    if (P.tiles > 2 * cus) {
+        // Up to eight tiles per CU: one workgroup per CU with a wave per tile.
+        // More: two workgroups of four waves per CU (the faster shape when
+        // every wave walks several tiles).
+        const bool many = P.tiles > 8 * cus;
+        const int per_cu = many ? 2 : 1;
+        waves = many ? 4 : (P.tiles + cus - 1) / cus;
+        grid = (P.tiles + waves - 1) / waves;
+        if (grid > cus * per_cu) grid = cus * per_cu;
+    }
+    const int threads = 64 * waves;
+    const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
     switch (xf) {
-        case X_ENGINE: return launch_xf<X_ENGINE>(P, nbpl, grid, stream);
-        case X_Q8_0: return launch_xf<X_Q8_0>(P, nbpl, grid, stream);
-        case X_F32: return launch_xf<X_F32>(P, nbpl, grid, stream);
+        case X_ENGINE: return launch_layout<X_ENGINE>(P, plain, grid, threads, lds, stream);
+        case X_Q8_0: return launch_layout<X_Q8_0>(P, plain, grid, threads, lds, stream);
+        case X_F32: return launch_layout<X_F32>(P, plain, grid, threads, lds, stream);
         default: return hipErrorInvalidValue;
     }
 }
