@@ -64,23 +64,60 @@ def build_chain(torch, kv, cf):
     return chain, mats, xs, ys, steps
 
 
-def time_chain(torch, kv, steps, n, n_steps, warmup):
+def time_chain(torch, kv, steps, n, n_steps, warmup, graph=True):
+    """ms per decode step of the dependent chain (w4a8_chain_gemv: 65 stream-ordered
+    fused quantize + GEMV launches). graph=True captures one step into a HIP graph
+    and replays it, which is how a decode loop would issue it."""
+    import ctypes
+    L = kv.lib()
+    ptr = ctypes.cast(steps, ctypes.c_void_p)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for _ in range(max(1, warmup)):
+            kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s.cuda_stream))
+    torch.cuda.synchronize()
+    run = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, torch.cuda.current_stream().cuda_stream))
+        with torch.cuda.stream(s):
+            for _ in range(max(1, warmup)):
+                g.replay()
+        run = g.replay
+    else:
+        def run():
+            kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s.cuda_stream))
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(s):
+        start.record(s)
+        for _ in range(n_steps):
+            run()
+        end.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / n_steps, wall
+
+
+def time_batch(torch, kv, steps, n, n_steps, warmup):
+    """ms per step with the step's 65 GEMVs in one w4a8_gemv_batch launch (no order
+    between the matrices of a step; steps stay ordered)."""
     import ctypes
     L = kv.lib()
     ptr = ctypes.cast(steps, ctypes.c_void_p)
     stream = torch.cuda.current_stream().cuda_stream
-    for _ in range(warmup):
-        kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, stream))
+    for _ in range(max(1, warmup)):
+        kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, stream))
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
     start.record()
     for _ in range(n_steps):
-        kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, stream))
+        kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, stream))
     end.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / n_steps, wall
+    return start.elapsed_time(end) / n_steps
 
 
 def time_gemv(torch, kv, cf, m, reps_min=200):
@@ -167,19 +204,27 @@ def main() -> int:
     chain, mats, xs, ys, steps = build_chain(torch, kv, cf)
     n = len(chain)
     chain_bytes = cf.chain_algorithmic_bytes()
-    log(f"timing {args.steps} steps after {args.warmup} warm-up steps")
-    ms_per_step, wall = time_chain(torch, kv, steps, n, args.steps, args.warmup)
+    log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay)")
+    ms_per_step, wall = time_chain(torch, kv, steps, n, args.steps, args.warmup, graph=True)
+    ms_stream, _ = time_chain(torch, kv, steps, n, max(10, args.steps // 4), args.warmup, graph=False)
     tok_s = 1e3 / ms_per_step
-    achieved = chain_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"chain: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {achieved:.0f} GB/s")
+    chain_gbs = chain_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"chain: {ms_per_step * 1e3:.1f} us/step ({ms_stream * 1e3:.1f} us/step without the graph), "
+        f"{tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s")
+
+    ms_batch = time_batch(torch, kv, steps, n, args.steps, args.warmup)
+    batch_gbs = chain_bytes / (ms_batch * 1e-3) / 1e9
+    log(f"batch: {ms_batch * 1e3:.1f} us/step, {batch_gbs:.0f} GB/s (one launch, no order inside a step)")
 
     gemv = {}
-    if not args.no_gemv:
-        for m in (cf.O_PROJ,) + cf.LAYER_SHAPES + (cf.LM_HEAD,):
-            r = time_gemv(torch, kv, cf, m)
-            gemv[m.name if m is not cf.O_PROJ else "o_proj_config0"] = r
-            log(f"gemv {m.name} {r['shape']}: {r['us']} us, {r['gbps']} GB/s")
-            torch.cuda.empty_cache()
+    shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES
+    for m in shapes:
+        r = time_gemv(torch, kv, cf, m)
+        gemv[m.name if m is not cf.O_PROJ else "o_proj_config0"] = r
+        log(f"gemv {m.name} {r['shape']}: {r['us']} us, {r['gbps']} GB/s")
+        torch.cuda.empty_cache()
+    lm = gemv["lm_head"]
+    lm_gbs = cf.LM_HEAD.algorithmic_bytes / (lm["us"] * 1e-6) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -205,10 +250,16 @@ def main() -> int:
                                "activation re-quantized to Q8_0 before every matrix",
                    "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
                    "algorithmic_bytes_per_step": chain_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode step (65 fused quantize+GEMV launches)",
-                     "bytes_per_launch": chain_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_m1_kernel<X_ENGINE> on the LM head 128256x2048 (3 rotating weight copies)",
+                     "bytes_per_launch": cf.LM_HEAD.algorithmic_bytes, "us_per_launch": lm["us"]},
+        "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "us_per_step_no_graph": round(ms_stream * 1e3, 2),
+                  "gbps": round(chain_gbs, 1), "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+                  "launches_per_step": n, "dependency": "matrix j+1 starts after matrix j's output is complete"},
+        "batch": {"us_per_step": round(ms_batch * 1e3, 2), "gbps": round(batch_gbs, 1),
+                  "hbm_frac": round(batch_gbs / HBM_PEAK_GBS, 4), "launches_per_step": 1,
+                  "dependency": "none inside a step (w4a8_gemv_batch); steps in order"},
         "gemv": gemv,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),

@@ -113,6 +113,15 @@ typedef struct w4a8_chain_step {
  * own, byte for byte. 1 <= n <= W4A8_CHAIN_MAX_STEPS. */
 int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream);
 
+/* The same n GEMVs with no order between them, in one launch: every matrix
+ * streams at once, so small matrices no longer pay a launch and a latency
+ * tail each. Each y equals w4a8_gemv_f32 on its own, byte for byte. For
+ * matrices that share an activation or are consumed together -- the
+ * reference fuses q|k|v and gate|up into single matrices for this reason
+ * (board/tp/tp_llama.cpp:258-268) -- or for a batch of independent
+ * requests. Outputs must not overlap inputs. 1 <= n <= W4A8_CHAIN_MAX_STEPS. */
+int w4a8_gemv_batch(const w4a8_chain_step *steps, int n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

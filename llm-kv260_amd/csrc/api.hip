@@ -132,4 +132,12 @@ int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream) {
     return hip_status(launch_chain(steps, n, (hipStream_t)stream));
 }
 
+int w4a8_gemv_batch(const w4a8_chain_step *steps, int n, void *stream) {
+    if (!steps) return W4A8_ERR_NULL;
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
+    for (int i = 0; i < n; ++i)
+        if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
+    return hip_status(launch_gemv_batch(steps, n, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -58,6 +58,24 @@ struct GemvParams {
     int paired;       // v2 port layout
 };
 
+constexpr int BATCH_THREADS = 256;          // four waves per workgroup
+constexpr int BATCH_TILES_PER_WAVE = 6;
+
+struct BatchEntry {
+    const uint8_t *w;
+    const void *x;
+    float *y;
+    int rows;
+    int k;
+};
+
+// Passed by value (kernel arguments): 32 B per entry.
+struct BatchParams {
+    int n;
+    int tiles_per_block;
+    BatchEntry e[W4A8_CHAIN_MAX_STEPS];
+};
+
 // Address of chunk c of row r (r counted over the whole matrix).
 template <bool PLAIN>
 __device__ __forceinline__ const uint8_t *chunk_ptr(const GemvParams &P, int r, int c) {
@@ -220,10 +238,10 @@ __device__ __forceinline__ void wave_sync_lds() {
 }
 
 // LDS layout (dynamic): per-wave slabs [waves][9216] | x int8[K] | x scale
-// f32[nb] | x sum i32[nb].
+// f32[nb] | x sum i32[nb]. `block` / `nblocks` are this workgroup's index and
+// the number of workgroups sharing the matrix.
 template <int XF, bool PLAIN>
-__global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+__device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -257,8 +275,8 @@ __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
     // 1. Activation loads first, then the first DEPTH tiles.
     XRaw<XF> xr;
     if (tid < nb) x_load<XF>(P.x, P.k, tid, xr);
-    int tile = blockIdx.x * waves + wave;
-    const int tstride = gridDim.x * waves;
+    int tile = block * waves + wave;
+    const int tstride = nblocks * waves;
     Tile buf[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
@@ -352,6 +370,53 @@ __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
 }
 
 template <int XF, bool PLAIN>
+__global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    gemv_m1_body<XF, PLAIN>(P, blockIdx.x, gridDim.x, lds);
+}
+
+__host__ __device__ inline void derive_plain(GemvParams &P, const uint8_t *w, const void *x, float *y, int rows, int k) {
+    P.seg[0] = P.seg[1] = P.seg[2] = P.seg[3] = w;
+    P.x = x;
+    P.y = y;
+    P.seg_rows = rows;
+    P.nseg = 1;
+    P.k = k;
+    P.rows = rows;
+    P.C = k >> 8;
+    P.rpw = 64 / P.C;
+    P.tiles = (rows + P.rpw - 1) / P.rpw;
+    P.paired = 0;
+}
+
+// Workgroups of one batch entry: enough that each wave owns about
+// BATCH_TILES_PER_WAVE tiles.
+__host__ __device__ inline int batch_blocks(int rows, int k, int tiles_per_block) {
+    const int rpw = 64 / (k >> 8);
+    const int tiles = (rows + rpw - 1) / rpw;
+    return (tiles + tiles_per_block - 1) / tiles_per_block;
+}
+
+// Many independent GEMVs in one launch: workgroups [b_j, b_j + n_j) serve
+// entry j (n_j = batch_blocks of its shape), each exactly as the
+// single-matrix kernel would with a grid of n_j workgroups.
+// Two waves per SIMD (two workgroups per CU), as the single-matrix kernel runs.
+__global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemv_batch_kernel(BatchParams B) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int b = blockIdx.x;
+    int j = 0, nblk = 0;
+    for (; j < B.n; ++j) {
+        nblk = batch_blocks(B.e[j].rows, B.e[j].k, B.tiles_per_block);
+        if (b < nblk) break;
+        b -= nblk;
+    }
+    if (j >= B.n) return;
+    GemvParams P;
+    derive_plain(P, B.e[j].w, B.e[j].x, B.e[j].y, B.e[j].rows, B.e[j].k);
+    gemv_m1_body<X_F32, true>(P, b, nblk, lds);
+}
+
+template <int XF, bool PLAIN>
 hipError_t launch_xf(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
     // Dynamic LDS above the default 64 KB must be allowed per kernel once.
     static bool lds_allowed = false;
@@ -428,6 +493,33 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
         case X_F32: return launch_layout<X_F32>(P, plain, grid, threads, lds, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream) {
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return hipErrorInvalidValue;
+    BatchParams B{};
+    B.n = n;
+    B.tiles_per_block = BATCH_TILES_PER_WAVE * (BATCH_THREADS / 64);
+    long blocks = 0;
+    int max_k = 0;
+    for (int i = 0; i < n; ++i) {
+        const int k = steps[i].k;
+        if (k < 256 || k % 256 || k > MAX_K_M1 || steps[i].rows < 1) return hipErrorInvalidValue;
+        B.e[i] = BatchEntry{static_cast<const uint8_t *>(steps[i].w), steps[i].x, steps[i].y, steps[i].rows, k};
+        blocks += batch_blocks(steps[i].rows, k, B.tiles_per_block);
+        if (k > max_k) max_k = k;
+    }
+    if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
+    const size_t lds = (size_t)(BATCH_THREADS / 64) * TILE_BYTES + (size_t)(max_k / QK) * 40;
+    static bool lds_allowed = false;
+    if (!lds_allowed) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BUDGET);
+        if (e != hipSuccess) return e;
+        lds_allowed = true;
+    }
+    hipLaunchKernelGGL(gemv_batch_kernel, dim3((unsigned)blocks), dim3(BATCH_THREADS), lds, stream, B);
+    return hipGetLastError();
 }
 
 hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream) {

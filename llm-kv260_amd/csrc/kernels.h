@@ -53,6 +53,9 @@ namespace w4a8 {
 // The decode chain: one GEMV per step, in order, x quantized inside.
 hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream);
 
+// The same GEMVs with no order between them, in one launch.
+hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream);
+
 // w: float32[rows][K] -> Q4_0 rows.
 hipError_t launch_quantize_q4_0(const float *w, int rows, int k, uint8_t *out, hipStream_t stream);
 

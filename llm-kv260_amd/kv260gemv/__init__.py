@@ -37,7 +37,7 @@ EXPORTS = (
     "w4a8_q4_0_row_bytes", "w4a8_engine_x_bytes", "w4a8_q8_0_row_bytes",
     "w4a8_gemv", "w4a8_gemv_q8_0", "w4a8_gemv_f32", "w4a8_gemv_quarters",
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
-    "w4a8_chain_gemv",
+    "w4a8_chain_gemv", "w4a8_gemv_batch",
     # gemv_dev.h
     "gemv_dev_open", "gemv_dev_open_named", "gemv_dev_close", "gemv_dev_run",
     "gemv_dev_start", "gemv_dev_wait", "gemv_dev_start4",
@@ -92,8 +92,9 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).restype = i
     L.w4a8_gemm.argtypes = [p, p, p, i, i, i, p]
     L.w4a8_gemm.restype = i
-    L.w4a8_chain_gemv.argtypes = [p, i, p]
-    L.w4a8_chain_gemv.restype = i
+    for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
+        getattr(L, f).argtypes = [p, i, p]
+        getattr(L, f).restype = i
     _lib = L
     return L
 

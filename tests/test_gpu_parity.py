@@ -257,6 +257,58 @@ def test_chain_equals_each_step_alone(gpu):
         assert_bytes_equal(host(ys[i]), wants[i], f"chain step {i}")
 
 
+def _steps(gpu, shapes, seed0):
+    import ctypes
+    mats, xs, ys, wants = [], [], [], []
+    for i, (rows, k) in enumerate(shapes):
+        w, x, blocks, xq, xd = _case(rows, k, seed0 + i, seed0 + 100 + i)
+        mats.append(dev(blocks))
+        xs.append(dev(x))
+        ys.append(poisoned_f32(rows))
+        wants.append(C.gemv_q4_0(blocks, k, xq, xd))
+
+    class Step(ctypes.Structure):
+        _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                    ("rows", ctypes.c_int), ("k", ctypes.c_int)]
+
+    steps = (Step * len(shapes))(*[Step(mats[i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(),
+                                        shapes[i][0], shapes[i][1]) for i in range(len(shapes))])
+    return steps, (mats, xs), ys, wants
+
+
+@pytest.mark.parametrize("shapes", [
+    [(96, 2048), (64, 2048), (512, 2048), (64, 8192), (300, 2048), (48, 2048)],
+    [(1, 256)],
+    [(3072, 2048), (2048, 2048), (16384, 2048), (2048, 8192), (5000, 2048)],
+    [(7, 16384), (33, 1024), (257, 2304), (1000, 4096)] * 3,
+])
+def test_batch_equals_each_gemv_alone(gpu, shapes):
+    """w4a8_gemv_batch: every matrix in one launch, each byte-equal to the oracle."""
+    import ctypes
+    import torch
+    steps, keep, ys, wants = _steps(gpu, shapes, 600)
+    stream = torch.cuda.current_stream().cuda_stream
+    gpu.check("w4a8_gemv_batch", gpu.lib().w4a8_gemv_batch(ctypes.cast(steps, ctypes.c_void_p), len(shapes), stream))
+    for i in range(len(shapes)):
+        assert_bytes_equal(host(ys[i]), wants[i], f"batch entry {i} {shapes[i]}")
+
+
+def test_batch_rejects_bad_steps(gpu):
+    import ctypes
+    import torch
+    steps, keep, ys, wants = _steps(gpu, [(64, 2048), (64, 2048)], 700)
+    L = gpu.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    steps[1].k = 2000
+    assert L.w4a8_gemv_batch(ctypes.cast(steps, ctypes.c_void_p), 2, stream) == -2
+    steps[1].k = 2048
+    steps[0].y = None
+    assert L.w4a8_gemv_batch(ctypes.cast(steps, ctypes.c_void_p), 2, stream) == -1
+    assert L.w4a8_gemv_batch(ctypes.cast(steps, ctypes.c_void_p), 0, stream) == -2
+    assert L.w4a8_gemv_batch(ctypes.cast(steps, ctypes.c_void_p), 97, stream) == -2
+    torch.cuda.synchronize()
+
+
 # ------------------------------------------------------------ C ABI errors
 
 def test_c_abi_rejects_bad_arguments_on_device(gpu):
