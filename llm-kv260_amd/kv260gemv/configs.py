@@ -45,12 +45,28 @@ class Matrix:
 def normal_f32(shape, seed: int, scale: float | None = None) -> np.ndarray:
     z = np.random.default_rng(seed).standard_normal(shape)
     if scale is not None:
-        z = z * scale
+        z *= scale          # in place: the same float64 products as z * scale
     return z.astype(np.float32)
 
 
 def weights(m: Matrix) -> np.ndarray:
     return normal_f32((m.rows, m.k), m.w_seed, W_SCALE)
+
+
+def weight_chunks(m: Matrix, rows_per_chunk: int = 4096):
+    """The rows of weights(m) in consecutive chunks: (first_row, float32 [r, K]).
+
+    The generator's stream continues across calls, so the chunks concatenate
+    to exactly weights(m); one float64 buffer is reused, so large matrices
+    (the 128256-row LM head) never hold more than a chunk in memory."""
+    rng = np.random.default_rng(m.w_seed)
+    buf = np.empty((rows_per_chunk, m.k), np.float64)
+    for r0 in range(0, m.rows, rows_per_chunk):
+        r = min(rows_per_chunk, m.rows - r0)
+        z = buf[:r]
+        rng.standard_normal(out=z)
+        z *= W_SCALE
+        yield r0, z.astype(np.float32)
 
 
 def activation(m: Matrix) -> np.ndarray:

@@ -204,5 +204,5 @@ def normal_f32(shape, seed: int, scale: float | None = None) -> np.ndarray:
     """
     z = np.random.default_rng(seed).standard_normal(shape)
     if scale is not None:
-        z = z * scale
+        z *= scale
     return z.astype(_F32)
