@@ -1,21 +1,35 @@
 """Benchmark of the MI355X W4A8 engine on the Llama-3.2-1B decode GEMV chain.
 
-    python bench.py [--gpus 1] [--steps 400] [--warmup 20] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 400] [--warmup 20] [--no-cpu] [--no-gemv]
 
 One step = one token's 65 W4A8 GEMVs (16 x q|k|v 3072x2048, o 2048x2048,
 gate|up 16384x2048, down 2048x8192, then the LM head 128256x2048), each
-preceded by the Q8_0 quantization of a float32 activation, in order, with
-weights (695,107,584 bytes of Q4_0) resident in HBM. The chain alone is
-larger than the 256 MB Infinity Cache, so every step streams from HBM.
+preceded by the Q8_0 quantization of a float32 activation, in order: matrix
+j+1 starts after matrix j's output is complete, as in a decode. The step is
+issued by w4a8_chain_gemv (65 launches of the fused quantize + GEMV kernel),
+captured once into a HIP graph and replayed. Weights (695,107,584 bytes of
+Q4_0) are resident in HBM; the chain alone is larger than the 256 MB Infinity
+Cache, so every step streams from HBM.
 
-Prints one JSON line: chain tokens/s (value), the roofline of the chain
-kernel, per-GEMV microseconds and GB/s at each layer shape and at the LM head
-(weights rotated past the Infinity Cache), and the CPU baseline.
+Prints one JSON line. Besides the chain (value), it reports:
+  roofline     the chain's kernel (the fused quantize + GEMV, 65 launches per
+               step): average algorithmic bytes per launch / average launch
+               duration, both over the timed region (HIP events on the launch
+               stream around the graph replays)
+  batch        the same 65 GEMVs per step in one w4a8_gemv_batch launch (no
+               order inside a step)
+  gemv         microseconds per GEMV at every shape, weights rotated past the
+               Infinity Cache, launched back to back from a HIP graph
+  gemm         the M > 1 sweep (M = 1 .. 64) at gate|up and down
+  cpu_baseline the NumPy restatement of the contract on one core, and the
+               C restatement on all cores, over one decode step
+All launches come from C through the library's ABI; Python only sets them up.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -25,35 +39,34 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "llm-kv260_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
-ROTATE_BYTES = 512 << 20       # >= 2 x the 256 MB Infinity Cache
+ROTATE_BYTES = 600 << 20       # > 2 x the 256 MB Infinity Cache
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def device_weights(torch, kv, m):
-    """Q4_0 blocks of an N(0, 0.02) fp32 matrix drawn with the device RNG (seeded by
-    the matrix's weight seed) and quantized by the engine's own Q4_0 kernel."""
+class CStep(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("rows", ctypes.c_int), ("k", ctypes.c_int)]
+
+
+def device_weights(torch, kv, rows, k, seed):
+    """Q4_0 blocks of an N(0, 0.02) fp32 matrix drawn with the device RNG and
+    quantized by the engine's own Q4_0 kernel."""
     g = torch.Generator(device="cuda")
-    g.manual_seed(m.w_seed)
-    w = torch.randn((m.rows, m.k), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    g.manual_seed(seed)
+    w = torch.randn((rows, k), generator=g, device="cuda", dtype=torch.float32) * 0.02
     blocks = kv.quantize_q4_0(w)
     del w
     return blocks
 
 
 def build_chain(torch, kv, cf):
-    import ctypes
-
-    class CStep(ctypes.Structure):
-        _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
-                    ("rows", ctypes.c_int), ("k", ctypes.c_int)]
-
     chain = cf.decode_chain()
     mats, xs, ys = [], [], []
     for i, m in enumerate(chain):
-        mats.append(device_weights(torch, kv, m))
+        mats.append(device_weights(torch, kv, m.rows, m.k, m.w_seed))
         xs.append(torch.from_numpy(cf.activation(m)).cuda())
         ys.append(torch.empty(m.rows, dtype=torch.float32, device="cuda"))
         if i % 16 == 15:
@@ -64,89 +77,79 @@ def build_chain(torch, kv, cf):
     return chain, mats, xs, ys, steps
 
 
-def time_chain(torch, kv, steps, n, n_steps, warmup, graph=True):
-    """ms per decode step of the dependent chain (w4a8_chain_gemv: 65 stream-ordered
-    fused quantize + GEMV launches). graph=True captures one step into a HIP graph
-    and replays it, which is how a decode loop would issue it."""
-    import ctypes
-    L = kv.lib()
-    ptr = ctypes.cast(steps, ctypes.c_void_p)
-    s = torch.cuda.Stream()
-    with torch.cuda.stream(s):
-        for _ in range(max(1, warmup)):
-            kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s.cuda_stream))
+def graph_of(torch, stream, calls):
+    """Capture calls (each takes a hipStream_t) into a HIP graph on `stream`."""
+    with torch.cuda.stream(stream):
+        for c in calls:                       # eager once: kernel attributes are set outside capture
+            c(stream.cuda_stream)
     torch.cuda.synchronize()
-    run = None
-    if graph:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, torch.cuda.current_stream().cuda_stream))
-        with torch.cuda.stream(s):
-            for _ in range(max(1, warmup)):
-                g.replay()
-        run = g.replay
-    else:
-        def run():
-            kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s.cuda_stream))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        st = torch.cuda.current_stream().cuda_stream
+        for c in calls:
+            c(st)
+    return g
+
+
+def time_replays(torch, stream, g, n, warmup):
+    """ms per replay over exactly n replays, synchronized on both sides."""
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    with torch.cuda.stream(s):
-        start.record(s)
-        for _ in range(n_steps):
-            run()
-        end.record(s)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(n):
+            g.replay()
+        end.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / n_steps, wall
+    return start.elapsed_time(end) / n, time.perf_counter() - t0
 
 
-def time_batch(torch, kv, steps, n, n_steps, warmup):
-    """ms per step with the step's 65 GEMVs in one w4a8_gemv_batch launch (no order
-    between the matrices of a step; steps stay ordered)."""
-    import ctypes
+def time_gemv(torch, kv, cf, m, stream):
+    """us per GEMV (engine-layout x) at one shape: back-to-back launches from a HIP
+    graph over rotating weight copies (>= 600 MB; 3 x 148 MB for the LM head)."""
     L = kv.lib()
-    ptr = ctypes.cast(steps, ctypes.c_void_p)
-    stream = torch.cuda.current_stream().cuda_stream
-    for _ in range(max(1, warmup)):
-        kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, stream))
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(n_steps):
-        kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, stream))
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / n_steps
-
-
-def time_gemv(torch, kv, cf, m, reps_min=200):
-    """us per GEMV (engine-layout x) over rotating copies of one matrix, >= 512 MB in total."""
-    base = device_weights(torch, kv, m)
-    copies = max(3, -(-ROTATE_BYTES // m.weight_bytes))
-    if m.rows * m.k >= 128256 * 2048:
-        copies = 3
+    base = device_weights(torch, kv, m.rows, m.k, 7)
+    copies = 3 if m.weight_bytes > (100 << 20) else max(3, -(-ROTATE_BYTES // m.weight_bytes))
     mats = [base] + [base.clone() for _ in range(copies - 1)]
     x = kv.quantize_q8_0_engine(torch.from_numpy(cf.activation(m)).cuda())
     y = torch.empty(m.rows, dtype=torch.float32, device="cuda")
-    reps = max(reps_min, copies * 2)
-    for i in range(copies):                              # warm-up
-        kv.gemv_engine(mats[i], m.k, x, out=y)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for r in range(reps):
-        kv.gemv_engine(mats[r % copies], m.k, x, out=y)
-    end.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1e3 / reps
-    del mats
-    return {"shape": f"{m.rows}x{m.k}", "us": round(us, 3),
-            "gbps": round(m.algorithmic_bytes / us / 1e3, 1),
+    launches = max(copies, 30)
+    calls = [(lambda w: (lambda s: kv.check("w4a8_gemv", L.w4a8_gemv(w.data_ptr(), x.data_ptr(), y.data_ptr(),
+                                                                    m.rows, m.k, s))))(mats[i % copies])
+             for i in range(launches)]
+    g = graph_of(torch, stream, calls)
+    ms, _ = time_replays(torch, stream, g, 10, 2)
+    us = ms * 1e3 / launches
+    del g, mats, base
+    return {"shape": f"{m.rows}x{m.k}", "us": round(us, 3), "gbps": round(m.algorithmic_bytes / us / 1e3, 1),
             "weight_copies": copies, "rotated_mb": round(copies * m.weight_bytes / 2**20, 1)}
 
 
-def cpu_baseline(kv, torch, chain, mats, xs, budget_s=30.0):
+def time_gemm(torch, kv, cf, m, mrows, stream):
+    """us per M > 1 GEMM (engine-layout activation rows), rotating weight copies."""
+    L = kv.lib()
+    base = device_weights(torch, kv, m.rows, m.k, 8)
+    copies = max(3, -(-ROTATE_BYTES // m.weight_bytes))
+    mats = [base] + [base.clone() for _ in range(copies - 1)]
+    xr = kv.quantize_q8_0_engine(torch.from_numpy(cf.gemm_activation(mrows, m.k)).cuda())
+    y = torch.empty((mrows, m.rows), dtype=torch.float32, device="cuda")
+    calls = [(lambda w: (lambda s: kv.check("w4a8_gemm", L.w4a8_gemm(w.data_ptr(), xr.data_ptr(), y.data_ptr(),
+                                                                    mrows, m.rows, m.k, s))))(mats[i])
+             for i in range(copies)]
+    g = graph_of(torch, stream, calls)
+    ms, _ = time_replays(torch, stream, g, 5, 1)
+    us = ms * 1e3 / copies
+    nbytes = m.weight_bytes + mrows * (m.k + m.k // 8) + 4 * mrows * m.rows
+    del g, mats, base
+    return {"shape": f"{m.rows}x{m.k}", "m": mrows, "us": round(us, 3), "gbps": round(nbytes / us / 1e3, 1),
+            "tops": round(2 * mrows * m.rows * m.k / us / 1e6, 2)}
+
+
+def cpu_baseline(chain, mats, xs, budget_s=30.0):
     """One decode step through the NumPy restatement of q4_0.py (1 core), and the
     same step through the scalar C restatement with OpenMP over rows (all cores)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -187,7 +190,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-gemv", action="store_true", help="skip the per-GEMV measurements")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the per-shape GEMV and GEMM timings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine runs every matrix unsplit on one GPU; --gpus {args.gpus} is not "
@@ -200,36 +203,48 @@ def main() -> int:
 
     kv.require_device(0)
     torch.cuda.set_device(0)
+    L = kv.lib()
+    stream = torch.cuda.Stream()
     log("building the 65-matrix decode chain on the device")
     chain, mats, xs, ys, steps = build_chain(torch, kv, cf)
     n = len(chain)
     chain_bytes = cf.chain_algorithmic_bytes()
+    ptr = ctypes.cast(steps, ctypes.c_void_p)
+
     log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay)")
-    ms_per_step, wall = time_chain(torch, kv, steps, n, args.steps, args.warmup, graph=True)
-    ms_stream, _ = time_chain(torch, kv, steps, n, max(10, args.steps // 4), args.warmup, graph=False)
+    g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
+    ms_per_step, wall = time_replays(torch, stream, g_chain, args.steps, args.warmup)
     tok_s = 1e3 / ms_per_step
     chain_gbs = chain_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"chain: {ms_per_step * 1e3:.1f} us/step ({ms_stream * 1e3:.1f} us/step without the graph), "
-        f"{tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s")
+    log(f"chain: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s")
 
-    ms_batch = time_batch(torch, kv, steps, n, args.steps, args.warmup)
+    g_batch = graph_of(torch, stream, [lambda s: kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, s))])
+    ms_batch, _ = time_replays(torch, stream, g_batch, args.steps, args.warmup)
     batch_gbs = chain_bytes / (ms_batch * 1e-3) / 1e9
     log(f"batch: {ms_batch * 1e3:.1f} us/step, {batch_gbs:.0f} GB/s (one launch, no order inside a step)")
+    del g_chain, g_batch
 
-    gemv = {}
+    gemv, gemm = {}, []
     shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES
     for m in shapes:
-        r = time_gemv(torch, kv, cf, m)
+        r = time_gemv(torch, kv, cf, m, stream)
         gemv[m.name if m is not cf.O_PROJ else "o_proj_config0"] = r
         log(f"gemv {m.name} {r['shape']}: {r['us']} us, {r['gbps']} GB/s")
         torch.cuda.empty_cache()
+    if not args.no_gemv:
+        for m in cf.GEMM_SHAPES:
+            for mrows in cf.GEMM_M:
+                r = time_gemm(torch, kv, cf, m, mrows, stream)
+                gemm.append(dict(name=m.name, **r))
+                log(f"gemm {m.name} M={mrows}: {r['us']} us, {r['gbps']} GB/s, {r['tops']} TOP/s")
+            torch.cuda.empty_cache()
     lm = gemv["lm_head"]
-    lm_gbs = cf.LM_HEAD.algorithmic_bytes / (lm["us"] * 1e-6) / 1e9
+    lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
-        cpu = cpu_baseline(kv, torch, chain, mats, xs)
+        cpu = cpu_baseline(chain, mats, xs)
 
     out = {
         "metric": "1B-shape decode GEMV-chain tokens/s (W4A8 Q4_0 x Q8_0, 65 GEMVs per token)",
@@ -243,24 +258,32 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4xint8->int32, fp32 epilogue",
-        "data": "synthetic: Q4_0 weights from N(0,0.02) drawn with the device RNG per matrix seed and "
-                "quantized by the engine; fp32 N(0,1) activations, numpy-seeded per matrix",
+        "data": "synthetic: Q4_0 weights from N(0,0.02) drawn with the device RNG per matrix and quantized by "
+                "the engine; fp32 N(0,1) activations, numpy-seeded per matrix",
         "config": {"workload": "llama-3.2-1b decode GEMV chain: 16 x (qkv 3072x2048, o 2048x2048, "
                                "gate_up 16384x2048, down 2048x8192) + lm_head 128256x2048, M=1, "
-                               "activation re-quantized to Q8_0 before every matrix",
+                               "activation re-quantized to Q8_0 before every matrix, matrices in order",
                    "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
                    "algorithmic_bytes_per_step": chain_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_m1_kernel<X_ENGINE> on the LM head 128256x2048 (3 rotating weight copies)",
-                     "bytes_per_launch": cf.LM_HEAD.algorithmic_bytes, "us_per_launch": lm["us"]},
-        "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "us_per_step_no_graph": round(ms_stream * 1e3, 2),
-                  "gbps": round(chain_gbs, 1), "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4),
-                  "launches_per_step": n, "dependency": "matrix j+1 starts after matrix j's output is complete"},
+        "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_m1_kernel<X_F32> (fused Q8_0 quantize + GEMV), the chain's 65 launches",
+                     "bytes_per_launch": round(chain_bytes / n), "us_per_launch": round(ms_per_step * 1e3 / n, 3)},
+        "roofline_batch": {"achieved": round(batch_gbs, 1), "frac": round(batch_gbs / HBM_PEAK_GBS, 4),
+                           "unit": "GB/s", "kernel": "gemv_batch_kernel, one step's 65 GEMVs per launch",
+                           "bytes_per_launch": chain_bytes, "us_per_launch": round(ms_batch * 1e3, 3)},
+        "roofline_lm_head": {"achieved": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "unit": "GB/s",
+                             "kernel": "gemv_m1_kernel<X_ENGINE>, LM head 128256x2048, 3 rotating weight copies",
+                             "bytes_per_launch": cf.LM_HEAD.algorithmic_bytes, "us_per_launch": lm["us"]},
+        "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "gbps": round(chain_gbs, 1),
+                  "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4), "launches_per_step": n,
+                  "dependency": "matrix j+1 starts after matrix j's output is complete"},
         "batch": {"us_per_step": round(ms_batch * 1e3, 2), "gbps": round(batch_gbs, 1),
                   "hbm_frac": round(batch_gbs / HBM_PEAK_GBS, 4), "launches_per_step": 1,
+                  "tokens_per_s": round(1e3 / ms_batch, 1),
                   "dependency": "none inside a step (w4a8_gemv_batch); steps in order"},
         "gemv": gemv,
+        "gemm": gemm,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }

@@ -31,6 +31,8 @@
 //    the slab, and lane 8r + a of the wave reads term a of chunks 0 .. C-1 of
 //    row r and adds them one by one. The eight lane sums of a row then meet
 //    in a DPP adjacent-pair tree.
+#include <type_traits>
+
 #include "../../include/w4a8.h"
 #include "kernels.h"
 #include "q4_0_device.h"
@@ -58,8 +60,14 @@ struct GemvParams {
     int paired;       // v2 port layout
 };
 
-constexpr int BATCH_THREADS = 256;          // four waves per workgroup
-constexpr int BATCH_TILES_PER_WAVE = 6;
+#ifndef W4A8_BATCH_WAVES
+#define W4A8_BATCH_WAVES 4
+#endif
+#ifndef W4A8_BATCH_TILES_PER_WAVE
+#define W4A8_BATCH_TILES_PER_WAVE 12
+#endif
+constexpr int BATCH_THREADS = 64 * W4A8_BATCH_WAVES;
+constexpr int BATCH_TILES_PER_WAVE = W4A8_BATCH_TILES_PER_WAVE;
 
 struct BatchEntry {
     const uint8_t *w;
@@ -240,7 +248,21 @@ __device__ __forceinline__ void wave_sync_lds() {
 // LDS layout (dynamic): per-wave slabs [waves][9216] | x int8[K] | x scale
 // f32[nb] | x sum i32[nb]. `block` / `nblocks` are this workgroup's index and
 // the number of workgroups sharing the matrix.
-template <int XF, bool PLAIN>
+// Raw buffer store of one fp32 to y[row]; a lane whose offset is past the end
+// of y stores nothing (the buffer unit drops out-of-range writes). Every lane
+// issues the instruction, so the number of memory operations a wave has in
+// flight never depends on data, and the waits for the prefetched tiles stay
+// exact.
+constexpr int Y_DROP = 0x7ffffff0;
+constexpr uint32_t BUFFER_DWORD3 = 0x00020000;   // raw dword access on gfx9-family parts
+
+__device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t y, int byte_off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y, byte_off, 0, 0);
+}
+
+// ONE_PASS: a tile holds at most eight rows (K >= 2048), so one pass of the
+// ordered sums covers it and each lane stores at most one value per tile.
+template <int XF, bool PLAIN, bool ONE_PASS>
 __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
@@ -272,28 +294,31 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     }
 
     constexpr int DEPTH = depth_of<PLAIN>();
-    // 1. Activation loads first, then the first DEPTH tiles.
-    XRaw<XF> xr;
-    if (tid < nb) x_load<XF>(P.x, P.k, tid, xr);
     int tile = block * waves + wave;
     const int tstride = nblocks * waves;
-    Tile buf[DEPTH];
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-        if (tile + d * tstride < P.tiles) load_tile<PLAIN>(P, tile + d * tstride, lane, dr, col, pc, buf[d]);
+    const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
+    // Loads past the wave's last tile (the refills of its last round) read
+    // its first tile again: lines it already fetched, never a line every
+    // wave would hammer at once. Their data is never used.
+    const int home = tile < P.tiles ? tile : 0;
 
-    // 2. Stage the activation, then pull this lane's chunk column into registers.
-    if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s);
-    for (int b = tid + nthreads; b < nb; b += nthreads) {
-        XRaw<XF> xb;
-        x_load<XF>(P.x, P.k, b, xb);
-        x_stage<XF>(xb, b, s_q, s_d, s_s);
-    }
-    __syncthreads();
+    // 1. The activation. Its loads go out before any weight tile's; the
+    // staging below waits for them only.
+    XRaw<XF> xr;
+    x_load<XF>(P.x, P.k, tid < nb ? tid : 0, xr);
+
     uint32_t xv[8][8];
     float xd[8];
     int32_t xs[8];
-    {
+    // 2. Stage the activation, then pull this lane's chunk column into registers.
+    auto stage_x = [&]() {
+        if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s);
+        for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
+            XRaw<XF> xb;
+            x_load<XF>(P.x, P.k, b, xb);
+            x_stage<XF>(xb, b, s_q, s_d, s_s);
+        }
+        __syncthreads();
         const int cb = lane_live ? 8 * my_c : 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -304,12 +329,14 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             xd[j] = s_d[cb + j];
             xs[j] = s_s[cb + j];
         }
-    }
+    };
 
     const int acc_r = lane >> 3, acc_a = lane & 7;
+    const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * P.rows, BUFFER_DWORD3);
     // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
-    // slab -> ordered lane sums -> tree -> y; then the buffer is refilled.
-    auto step = [&](Tile &b) {
+    // slab -> ordered lane sums -> tree -> y; with REFILL the buffer then
+    // receives the tile DEPTH strides ahead while the terms are computed.
+    auto step = [&](Tile &b, auto refill) {
         u32x4 *wslab = reinterpret_cast<u32x4 *>(slab);
 #pragma unroll
         for (int p = 0; p < CHUNK_PIECES; ++p) wslab[64 * p + lane] = b.p[p];
@@ -323,8 +350,10 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                 w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
             }
         }
-        const int tn = tile + DEPTH * tstride;
-        if (tn < P.tiles) load_tile<PLAIN>(P, tn, lane, dr, col, pc, b);
+        if constexpr (decltype(refill)::value) {
+            const int tn = tile + DEPTH * tstride;
+            load_tile<PLAIN>(P, tn < P.tiles ? tn : home, lane, dr, col, pc, b);
+        }
         float t[8];
         chunk_terms(w, xv, xd, xs, t);
         wave_sync_lds();
@@ -339,7 +368,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         // The reads go eight at a time; a column past C contributes +0.0f,
         // which leaves the sum unchanged (it started at +0.0f, so it is never
         // -0.0f, and x + 0 = x for every other x).
-        for (int r = acc_r; r - acc_r < rpw; r += 8) {
+        auto lane_sum = [&](int r) {
             float acc = 0.0f;
             if (r < rpw) {
                 const float *src = s_t + r * C * 9 + acc_a;
@@ -351,28 +380,57 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                     for (int j = 0; j < 8; ++j) acc = acc + v[j];
                 }
             }
-            const float yv = tree8_dpp(acc);
-            const int row = tile * rpw + r;
-            if (r < rpw && acc_a == 0 && row < P.rows) P.y[row] = yv;
+            return acc;
+        };
+        if constexpr (ONE_PASS) {
+            const float yv = tree8_dpp(lane_sum(acc_r));
+            const int row = tile * rpw + acc_r;
+            store_y(y_rsrc, acc_r < rpw && acc_a == 0 && row < P.rows ? 4 * row : Y_DROP, yv);
+        } else {
+            for (int r = acc_r; r - acc_r < rpw; r += 8) {
+                const float yv = tree8_dpp(lane_sum(r));
+                const int row = tile * rpw + r;
+                if (r < rpw && acc_a == 0 && row < P.rows) P.y[row] = yv;
+            }
         }
         wave_sync_lds();
         tile += tstride;
     };
-    while (tile < P.tiles) {
-        step(buf[0]);
-        if (tile >= P.tiles) break;
-        step(buf[1]);
-        if constexpr (DEPTH == 3) {
-            if (tile >= P.tiles) break;
-            step(buf[2]);
+
+    // 3. Three straight-line paths, chosen per wave, so that every wait on
+    // the loads in flight is exact: no tile, one tile, or the DEPTH-deep
+    // pipeline (whole rounds with refills, then the remainder without).
+    using refill_t = std::true_type;
+    using last_t = std::false_type;
+    if (n_my >= 2) {
+        Tile buf[DEPTH];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int t = tile + d * tstride;
+            load_tile<PLAIN>(P, t < P.tiles ? t : home, lane, dr, col, pc, buf[d]);
         }
+        stage_x();
+        int done = 0;
+        for (; done + DEPTH <= n_my; done += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) step(buf[d], refill_t{});
+        }
+        if (done < n_my) step(buf[0], last_t{});
+        if (done + 1 < n_my) step(buf[1], last_t{});
+    } else if (n_my == 1) {
+        Tile b;
+        load_tile<PLAIN>(P, tile, lane, dr, col, pc, b);
+        stage_x();
+        step(b, last_t{});
+    } else {
+        stage_x();
     }
 }
 
-template <int XF, bool PLAIN>
+template <int XF, bool PLAIN, bool ONE_PASS>
 __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    gemv_m1_body<XF, PLAIN>(P, blockIdx.x, gridDim.x, lds);
+    gemv_m1_body<XF, PLAIN, ONE_PASS>(P, blockIdx.x, gridDim.x, lds);
 }
 
 __host__ __device__ inline void derive_plain(GemvParams &P, const uint8_t *w, const void *x, float *y, int rows, int k) {
@@ -401,6 +459,8 @@ __host__ __device__ inline int batch_blocks(int rows, int k, int tiles_per_block
 // entry j (n_j = batch_blocks of its shape), each exactly as the
 // single-matrix kernel would with a grid of n_j workgroups.
 // Two waves per SIMD (two workgroups per CU), as the single-matrix kernel runs.
+// ONE_PASS: every entry has K >= 2048 (at most eight rows per tile).
+template <bool ONE_PASS>
 __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemv_batch_kernel(BatchParams B) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int b = blockIdx.x;
@@ -413,21 +473,27 @@ __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2
     if (j >= B.n) return;
     GemvParams P;
     derive_plain(P, B.e[j].w, B.e[j].x, B.e[j].y, B.e[j].rows, B.e[j].k);
-    gemv_m1_body<X_F32, true>(P, b, nblk, lds);
+    gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, lds);
 }
 
-template <int XF, bool PLAIN>
-hipError_t launch_xf(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
+template <int XF, bool PLAIN, bool ONE_PASS>
+hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
     // Dynamic LDS above the default 64 KB must be allowed per kernel once.
     static bool lds_allowed = false;
     if (!lds_allowed) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BUDGET);
         if (e != hipSuccess) return e;
         lds_allowed = true;
     }
-    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN>), dim3(grid), dim3(threads), lds, stream, P);
+    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS>), dim3(grid), dim3(threads), lds, stream, P);
     return hipGetLastError();
+}
+
+template <int XF, bool PLAIN>
+hipError_t launch_xf(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
+    return P.rpw <= 8 ? launch_pass<XF, PLAIN, true>(P, grid, threads, lds, stream)
+                      : launch_pass<XF, PLAIN, false>(P, grid, threads, lds, stream);
 }
 
 template <int XF>
@@ -468,13 +534,15 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     const int cus = device_cu_count();
     const int nb = w.k / QK;
     const size_t x_lds = (size_t)nb * 40;
-    // Small matrices: one wave per workgroup and one workgroup per tile,
-    // spread over every CU (each stages its own copy of x in parallel).
-    // Larger ones: at most eight waves per CU (the register budget of three
-    // tiles per wave allows two waves per SIMD), every wave walking tiles
-    // with a stride of the whole grid.
-    int waves = 1;
-    int grid = P.tiles;
+    // Small matrices: one tile per wave, workgroups spread over every CU
+    // (each stages its own copy of x in parallel). Larger ones: at most eight
+    // waves per CU (the register budget of three tiles per wave allows two
+    // waves per SIMD), every wave walking tiles with a stride of the whole
+    // grid. Every shape has at least one thread per activation block, so the
+    // activation is staged in one pass (K / 32 blocks over 64 * waves threads).
+    const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;     // <= 8 for K <= 16384
+    int waves = min_waves;
+    int grid = (P.tiles + waves - 1) / waves;
     if (P.tiles > 2 * cus) {
         // Up to eight tiles per CU: one workgroup per CU with a wave per tile.
         // More: two workgroups of four waves per CU (the faster shape when
@@ -482,6 +550,7 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
         const bool many = P.tiles > 8 * cus;
         const int per_cu = many ? 2 : 1;
         waves = many ? 4 : (P.tiles + cus - 1) / cus;
+        if (waves < min_waves) waves = min_waves;
         grid = (P.tiles + waves - 1) / waves;
         if (grid > cus * per_cu) grid = cus * per_cu;
     }
@@ -495,31 +564,43 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     }
 }
 
-hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream) {
-    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return hipErrorInvalidValue;
-    BatchParams B{};
-    B.n = n;
-    B.tiles_per_block = BATCH_TILES_PER_WAVE * (BATCH_THREADS / 64);
+template <bool ONE_PASS>
+hipError_t launch_batch_pass(const BatchParams &B, int max_k, hipStream_t stream) {
     long blocks = 0;
-    int max_k = 0;
-    for (int i = 0; i < n; ++i) {
-        const int k = steps[i].k;
-        if (k < 256 || k % 256 || k > MAX_K_M1 || steps[i].rows < 1) return hipErrorInvalidValue;
-        B.e[i] = BatchEntry{static_cast<const uint8_t *>(steps[i].w), steps[i].x, steps[i].y, steps[i].rows, k};
-        blocks += batch_blocks(steps[i].rows, k, B.tiles_per_block);
-        if (k > max_k) max_k = k;
-    }
+    for (int i = 0; i < B.n; ++i) blocks += batch_blocks(B.e[i].rows, B.e[i].k, B.tiles_per_block);
     if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
     const size_t lds = (size_t)(BATCH_THREADS / 64) * TILE_BYTES + (size_t)(max_k / QK) * 40;
     static bool lds_allowed = false;
     if (!lds_allowed) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel<ONE_PASS>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BUDGET);
         if (e != hipSuccess) return e;
         lds_allowed = true;
     }
-    hipLaunchKernelGGL(gemv_batch_kernel, dim3((unsigned)blocks), dim3(BATCH_THREADS), lds, stream, B);
+    hipLaunchKernelGGL(gemv_batch_kernel<ONE_PASS>, dim3((unsigned)blocks), dim3(BATCH_THREADS), lds, stream, B);
     return hipGetLastError();
+}
+
+hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream) {
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return hipErrorInvalidValue;
+    // Entries with K >= 2048 (one pass of ordered sums per tile) and the rest
+    // go to the two instances of the kernel: one launch when all are alike.
+    BatchParams B[2] = {};
+    int max_k[2] = {0, 0};
+    for (int i = 0; i < n; ++i) {
+        const int k = steps[i].k;
+        if (k < 256 || k % 256 || k > MAX_K_M1 || steps[i].rows < 1) return hipErrorInvalidValue;
+        const int s = k >= 2048 ? 0 : 1;
+        B[s].e[B[s].n++] = BatchEntry{static_cast<const uint8_t *>(steps[i].w), steps[i].x, steps[i].y, steps[i].rows, k};
+        if (k > max_k[s]) max_k[s] = k;
+    }
+    for (int s = 0; s < 2; ++s) B[s].tiles_per_block = BATCH_TILES_PER_WAVE * (BATCH_THREADS / 64);
+    if (B[0].n) {
+        const hipError_t e = launch_batch_pass<true>(B[0], max_k[0], stream);
+        if (e != hipSuccess) return e;
+    }
+    if (B[1].n) return launch_batch_pass<false>(B[1], max_k[1], stream);
+    return hipSuccess;
 }
 
 hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream) {
