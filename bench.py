@@ -42,6 +42,22 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 ROTATE_BYTES = 600 << 20       # > 2 x the 256 MB Infinity Cache
 
 
+PMC_SUMMARY = os.path.join("profiles", "gemv_pmc_traffic_llama1b_decode.txt")
+
+
+def pmc_traffic():
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE, scaled by a plain copy of known size), or None when absent."""
+    try:
+        with open(os.path.join(ROOT, PMC_SUMMARY)) as f:
+            for line in f:
+                if line.startswith("JSON "):
+                    return json.loads(line[5:])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -191,6 +207,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the per-shape GEMV and GEMM timings")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="first copy MB of device memory once: a plain copy of known size whose "
+                         "FETCH_SIZE / WRITE_SIZE counters scale the kernels' HBM traffic")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine runs every matrix unsplit on one GPU; --gpus {args.gpus} is not "
@@ -205,6 +224,14 @@ def main() -> int:
     torch.cuda.set_device(0)
     L = kv.lib()
     stream = torch.cuda.Stream()
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration << 18, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.copy_calibration} MB")
+        del src, dst
     log("building the 65-matrix decode chain on the device")
     chain, mats, xs, ys, steps = build_chain(torch, kv, cf)
     n = len(chain)
@@ -241,6 +268,7 @@ def main() -> int:
     lm = gemv["lm_head"]
     lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 
+    traffic = pmc_traffic() or {}
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
@@ -266,14 +294,17 @@ def main() -> int:
                    "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
                    "algorithmic_bytes_per_step": chain_bytes},
         "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(chain_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("chain_traffic_bytes_per_launch"), "traffic_source": PMC_SUMMARY,
                      "kernel": "gemv_m1_kernel<X_F32> (fused Q8_0 quantize + GEMV), the chain's 65 launches",
                      "bytes_per_launch": round(chain_bytes / n), "us_per_launch": round(ms_per_step * 1e3 / n, 3)},
         "roofline_batch": {"achieved": round(batch_gbs, 1), "frac": round(batch_gbs / HBM_PEAK_GBS, 4),
                            "unit": "GB/s", "kernel": "gemv_batch_kernel, one step's 65 GEMVs per launch",
+                           "traffic": traffic.get("batch_traffic_bytes_per_launch"),
                            "bytes_per_launch": chain_bytes, "us_per_launch": round(ms_batch * 1e3, 3)},
         "roofline_lm_head": {"achieved": round(lm_gbs, 1), "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "unit": "GB/s",
                              "kernel": "gemv_m1_kernel<X_ENGINE>, LM head 128256x2048, 3 rotating weight copies",
+                             "traffic": traffic.get("lm_head_traffic_bytes_per_launch"),
                              "bytes_per_launch": cf.LM_HEAD.algorithmic_bytes, "us_per_launch": lm["us"]},
         "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "gbps": round(chain_gbs, 1),
                   "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4), "launches_per_step": n,

@@ -46,6 +46,20 @@ constexpr size_t LDS_BUDGET = 160 * 1024;   // per CU on gfx950
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Raw buffer accesses: the buffer unit range-checks every lane against the
+// resource's size, so a lane whose offset is out of range touches no memory
+// (a load returns zeros, a store is dropped). Loads and stores are then
+// issued by every lane on every path -- the number of memory operations a
+// wave has in flight never depends on data, and each wait is exact -- while
+// the lanes with nothing to do cost no traffic.
+constexpr int OUT_OF_RANGE = 0x7ffffff0;
+constexpr uint32_t BUFFER_DWORD3 = 0x00020000;   // raw dword access on gfx9-family parts
+constexpr int CACHE_NT = 2;                       // non-temporal (streamed once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, BUFFER_DWORD3);
+}
+
 struct GemvParams {
     const uint8_t *seg[4];
     const void *x;
@@ -119,21 +133,28 @@ struct XRaw<X_F32> {
     float4 v[8];
 };
 
+// Block b of the activation; a lane with live == false reads nothing.
 template <int XF>
-__device__ __forceinline__ void x_load(const void *x, int k, int b, XRaw<XF> &r) {
+__device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, XRaw<XF> &r) {
     if constexpr (XF == X_ENGINE) {
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(x) + 32 * b);
-        r.q0 = src[0];
-        r.q1 = src[1];
-        r.d = reinterpret_cast<const float *>(static_cast<const uint8_t *>(x) + k)[b];
+        const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(k + k / 8));
+        const int q_off = live ? 32 * b : OUT_OF_RANGE, d_off = live ? k + 4 * b : OUT_OF_RANGE;
+        r.q0 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off, 0, 0);
+        r.q1 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off + 16, 0, 0);
+        r.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xb, d_off, 0, 0));
     } else if constexpr (XF == X_Q8_0) {
-        const uint16_t *src = reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(x) + Q8_0_BYTES * b);
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(x) +
+                                                                 Q8_0_BYTES * (live ? b : 0));
 #pragma unroll
         for (int i = 0; i < 17; ++i) r.h[i] = src[i];
     } else {
-        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + 32 * b);
+        const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(4 * k));
+        const int off = live ? 128 * b : OUT_OF_RANGE;
 #pragma unroll
-        for (int m = 0; m < 8; ++m) r.v[m] = src[m];
+        for (int m = 0; m < 8; ++m) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xb, off + 16 * m, 0, 0);
+            r.v[m] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+        }
     }
 }
 
@@ -206,28 +227,22 @@ struct Tile {
 };
 
 // Load the nine pieces of `tile` (lane l: bytes 1024 p + 16 l of the tile).
+// Plain layout: a tile past the end of the matrix reads nothing, and the
+// pieces of the last tile past the matrix's last byte read zeros (their terms
+// are never stored). Board layouts: per-lane addresses; a tile past the end
+// must not be asked for (the callers pass the wave's own first tile instead).
 template <bool PLAIN>
 __device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lane, const int dr[9], const int col[9],
                                           const int pc[9], Tile &t) {
     if constexpr (PLAIN) {
         const size_t tile_bytes = (size_t)P.rpw * (size_t)P.C * CHUNK_BYTES;
         const size_t total = (size_t)P.rows * (size_t)P.C * CHUNK_BYTES;
-        const size_t off0 = (size_t)tile * tile_bytes;
-        const uint8_t *base = P.seg[0] + off0 + 16 * lane;
-        if (off0 + TILE_BYTES <= total) {
+        const size_t off0 = (size_t)__builtin_amdgcn_readfirstlane(tile) * tile_bytes;
+        const bool in = off0 < total;
+        const uint32_t n = in ? (uint32_t)(total - off0 < (size_t)TILE_BYTES ? total - off0 : (size_t)TILE_BYTES) : 0u;
+        const __amdgpu_buffer_rsrc_t tb = buffer_of(P.seg[0] + (in ? off0 : 0), n);
 #pragma unroll
-            for (int p = 0; p < CHUNK_PIECES; ++p)
-                t.p[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + 1024 * p));
-        } else {
-            // The last tile overhangs the matrix: pieces past the end read
-            // its first bytes instead (their terms are never stored).
-#pragma unroll
-            for (int p = 0; p < CHUNK_PIECES; ++p) {
-                const size_t off = off0 + 1024 * p + 16 * lane;
-                const uint8_t *g = off + 16 <= total ? P.seg[0] + off : P.seg[0];
-                t.p[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(g));
-            }
-        }
+        for (int p = 0; p < CHUNK_PIECES; ++p) t.p[p] = __builtin_amdgcn_raw_buffer_load_b128(tb, 1024 * p + 16 * lane, 0, CACHE_NT);
     } else {
         const int row0 = tile * P.rpw;
 #pragma unroll
@@ -253,9 +268,6 @@ __device__ __forceinline__ void wave_sync_lds() {
 // issues the instruction, so the number of memory operations a wave has in
 // flight never depends on data, and the waits for the prefetched tiles stay
 // exact.
-constexpr int Y_DROP = 0x7ffffff0;
-constexpr uint32_t BUFFER_DWORD3 = 0x00020000;   // raw dword access on gfx9-family parts
-
 __device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t y, int byte_off, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y, byte_off, 0, 0);
 }
@@ -297,15 +309,16 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     int tile = block * waves + wave;
     const int tstride = nblocks * waves;
     const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
-    // Loads past the wave's last tile (the refills of its last round) read
-    // its first tile again: lines it already fetched, never a line every
-    // wave would hammer at once. Their data is never used.
+    // Board layouts: loads past the wave's last tile (the refills of its last
+    // round) read its first tile again, lines it already fetched, never a
+    // line every wave would hammer at once; their data is never used. (The
+    // plain layout's out-of-range loads read nothing at all.)
     const int home = tile < P.tiles ? tile : 0;
 
     // 1. The activation. Its loads go out before any weight tile's; the
     // staging below waits for them only.
     XRaw<XF> xr;
-    x_load<XF>(P.x, P.k, tid < nb ? tid : 0, xr);
+    x_load<XF>(P.x, P.k, tid, tid < nb, xr);
 
     uint32_t xv[8][8];
     float xd[8];
@@ -315,7 +328,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s);
         for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
             XRaw<XF> xb;
-            x_load<XF>(P.x, P.k, b, xb);
+            x_load<XF>(P.x, P.k, b, true, xb);
             x_stage<XF>(xb, b, s_q, s_d, s_s);
         }
         __syncthreads();
@@ -352,7 +365,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         }
         if constexpr (decltype(refill)::value) {
             const int tn = tile + DEPTH * tstride;
-            load_tile<PLAIN>(P, tn < P.tiles ? tn : home, lane, dr, col, pc, b);
+            load_tile<PLAIN>(P, PLAIN || tn < P.tiles ? tn : home, lane, dr, col, pc, b);
         }
         float t[8];
         chunk_terms(w, xv, xd, xs, t);
@@ -385,7 +398,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
             const int row = tile * rpw + acc_r;
-            store_y(y_rsrc, acc_r < rpw && acc_a == 0 && row < P.rows ? 4 * row : Y_DROP, yv);
+            store_y(y_rsrc, acc_r < rpw && acc_a == 0 && row < P.rows ? 4 * row : OUT_OF_RANGE, yv);
         } else {
             for (int r = acc_r; r - acc_r < rpw; r += 8) {
                 const float yv = tree8_dpp(lane_sum(r));
@@ -407,7 +420,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             const int t = tile + d * tstride;
-            load_tile<PLAIN>(P, t < P.tiles ? t : home, lane, dr, col, pc, buf[d]);
+            load_tile<PLAIN>(P, PLAIN || t < P.tiles ? t : home, lane, dr, col, pc, buf[d]);
         }
         stage_x();
         int done = 0;

@@ -1,0 +1,156 @@
+"""The reference driver's ABI on the GPU, called exactly as board/tp and
+bench_gemv2.c call it: udmabuf pools with clean / invalidate around each call,
+the v1 engine's four quarters (gemv_dev_start4) and the v2 engine's
+fetch + MAC pair on the chunk-interleaved port layout (gemv2_dev.h), each
+compared byte for byte with the oracle. Outputs are poisoned with 0xAA in the
+pool first (board/kv260gemv/bench_gemv2.c:63)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import c_oracle as C
+import q4_0_oracle as O
+from gpu_helpers import assert_bytes_equal
+
+pytestmark = pytest.mark.gpu
+
+
+class Udmabuf(ctypes.Structure):
+    _fields_ = [("fd", ctypes.c_int), ("base", ctypes.c_void_p), ("phys", ctypes.c_uint64),
+                ("size", ctypes.c_size_t), ("used", ctypes.c_size_t)]
+
+
+class Dev(ctypes.Structure):
+    _fields_ = [("fd", ctypes.c_int), ("regs", ctypes.c_void_p)]
+
+
+class Dev2(ctypes.Structure):
+    _fields_ = [("fetch", Dev), ("mac", Dev)]
+
+
+u64, i32, vp = ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p
+
+
+@pytest.fixture(scope="module")
+def board(gpu):
+    os.environ["KV260GEMV_UDMABUF_SIZES"] = "udmabuf0=96M"
+    L = gpu.lib()
+    L.udmabuf_open.argtypes = [ctypes.POINTER(Udmabuf), ctypes.c_char_p]
+    L.udmabuf_alloc.argtypes = [ctypes.POINTER(Udmabuf), ctypes.c_size_t, ctypes.c_size_t]
+    L.udmabuf_alloc.restype = vp
+    L.udmabuf_clean.argtypes = [vp, ctypes.c_size_t]
+    L.udmabuf_invalidate.argtypes = [vp, ctypes.c_size_t]
+    L.udmabuf_close.argtypes = [ctypes.POINTER(Udmabuf)]
+    L.gemv_dev_open.argtypes = [ctypes.POINTER(Dev)]
+    L.gemv_dev_close.argtypes = [ctypes.POINTER(Dev)]
+    L.gemv_dev_run.argtypes = [ctypes.POINTER(Dev), u64, u64, u64, i32, i32]
+    L.gemv_dev_start4.argtypes = [ctypes.POINTER(Dev), ctypes.POINTER(u64), u64, u64, i32, i32]
+    L.gemv_dev_wait.argtypes = [ctypes.POINTER(Dev)]
+    for f in ("gemv2_dev_open", "gemv2_dev_close", "gemv2_fetch_wait", "gemv2_mac_wait", "gemv2_mac_idle",
+              "gemv2_drain"):
+        getattr(L, f).argtypes = [ctypes.POINTER(Dev2)]
+    L.gemv2_fetch_start.argtypes = [ctypes.POINTER(Dev2), ctypes.POINTER(u64), i32, i32]
+    L.gemv2_mac_start.argtypes = [ctypes.POINTER(Dev2), u64, u64, i32, i32]
+    pool = Udmabuf()
+    assert L.udmabuf_open(ctypes.byref(pool), b"udmabuf0") == 0
+    yield L, pool
+    L.udmabuf_close(ctypes.byref(pool))
+
+
+def _alloc(L, pool, data_or_size, align=4096):
+    n = data_or_size if isinstance(data_or_size, int) else len(data_or_size)
+    p = L.udmabuf_alloc(ctypes.byref(pool), n, align)
+    assert p, "pool full"
+    if not isinstance(data_or_size, int):
+        ctypes.memmove(p, np.ascontiguousarray(data_or_size).ctypes.data, n)
+    L.udmabuf_clean(p, n)
+    return p, pool.phys + (p - pool.base)
+
+
+def _poisoned_y(L, pool, rows):
+    return _alloc(L, pool, np.full(4 * rows, 0xAA, np.uint8))
+
+
+def _read_y(L, p, rows):
+    L.udmabuf_invalidate(p, 4 * rows)
+    return np.ctypeslib.as_array((ctypes.c_float * rows).from_address(p)).copy()
+
+
+def _case(rows, k, seed):
+    w = O.normal_f32((rows, k), seed, 0.02)
+    x = O.normal_f32((1, k), seed + 1)[0]
+    blocks = C.quantize_q4_0(w)
+    xq, xd = C.quantize_q8_0(x)
+    return blocks, C.pack_x_for_engine(xq, xd), C.gemv_q4_0(blocks, k, xq, xd)
+
+
+@pytest.mark.parametrize("rows,k", [(512, 2048), (64, 8192), (2048, 2048)])
+def test_v1_quarters_and_run(board, rows, k):
+    """gemv_dev_start4 over quarters at staggered pool addresses (tp_llama.cpp:105-119),
+    then gemv_dev_run over the same rows contiguous."""
+    L, pool = board
+    blocks, x_eng, want = _case(rows, k, 300 + rows)
+    q = rows // 4
+    d = Dev()
+    assert L.gemv_dev_open(ctypes.byref(d)) == 0
+    phys = []
+    for i in range(4):
+        L.udmabuf_alloc(ctypes.byref(pool), (16 << 10) * (i % 2), 16)    # ports 1 and 3 at +16 KB
+        phys.append(_alloc(L, pool, blocks[i * q:(i + 1) * q].reshape(-1), 64 << 10)[1])
+    _, xp = _alloc(L, pool, x_eng)
+    yp_host, yp = _poisoned_y(L, pool, rows)
+    L.gemv_dev_start4(ctypes.byref(d), (u64 * 4)(*phys), xp, yp, k, rows)
+    L.gemv_dev_wait(ctypes.byref(d))
+    assert_bytes_equal(_read_y(L, yp_host, rows), want, "gemv_dev_start4")
+
+    _, wp = _alloc(L, pool, blocks.reshape(-1), 64 << 10)
+    y2_host, y2 = _poisoned_y(L, pool, rows)
+    L.gemv_dev_run(ctypes.byref(d), wp, xp, y2, k, rows)
+    assert_bytes_equal(_read_y(L, y2_host, rows), want, "gemv_dev_run")
+    L.gemv_dev_close(ctypes.byref(d))
+    pool.used = 0
+
+
+def _chunk_offset(r, c, rows, k):
+    """The v2 layout formula of gemv2_dev.h (port-relative byte offset, port)."""
+    per_port = rows // 4
+    half = per_port // 2
+    chunks = k // 256
+    local = r % per_port
+    pair, second = local % half, local // half
+    return ((pair * chunks + c) * 2 + second) * 144, r // per_port
+
+
+@pytest.mark.parametrize("rows,k", [(768, 2048), (32, 256), (2048, 8192), (4096, 2048)])
+def test_v2_fetch_then_mac(board, rows, k):
+    """gemv2_fetch_start + gemv2_mac_start + gemv2_mac_wait on the chunk-interleaved
+    layout, as engine_t::gemv issues them (tp_llama.cpp:364-368)."""
+    L, pool = board
+    blocks, x_eng, want = _case(rows, k, 400 + rows)
+    chunks = k // 256
+    raw = blocks.reshape(rows, chunks, 144)
+    regions = [np.zeros(rows // 4 * chunks * 144, np.uint8) for _ in range(4)]
+    for r in range(rows):
+        for c in range(chunks):
+            off, port = _chunk_offset(r, c, rows, k)
+            regions[port][off:off + 144] = raw[r, c]
+    d2 = Dev2()
+    assert L.gemv2_dev_open(ctypes.byref(d2)) == 0
+    assert L.gemv2_mac_idle(ctypes.byref(d2)) == 1
+    L.gemv2_drain(ctypes.byref(d2))
+    phys = [_alloc(L, pool, reg, 64 << 10)[1] for reg in regions]
+    _, xp = _alloc(L, pool, x_eng)
+    y_host, yp = _poisoned_y(L, pool, rows)
+    L.gemv2_fetch_start(ctypes.byref(d2), (u64 * 4)(*phys), k, rows)
+    L.gemv2_fetch_wait(ctypes.byref(d2))
+    L.gemv2_mac_start(ctypes.byref(d2), xp, yp, k, rows)
+    L.gemv2_mac_wait(ctypes.byref(d2))
+    assert L.gemv2_mac_idle(ctypes.byref(d2)) == 1
+    assert_bytes_equal(_read_y(L, y_host, rows), want, "gemv2 fetch + mac")
+    L.gemv2_dev_close(ctypes.byref(d2))
+    pool.used = 0
