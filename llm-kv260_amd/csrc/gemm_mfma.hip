@@ -18,30 +18,36 @@
 // the low nibbles of block bytes 0..7 (g = 0) and 8..15 (g = 1), then the high
 // nibbles of bytes 0..7 (g = 2) and 8..15 (g = 3).
 //
-// Order without serialising K: the contract's accumulator a (0..7) of an
-// output adds the terms of blocks a, a + 8, a + 16, ... in that order, and
-// never sees another block. A workgroup's eight waves share an item (16 or 8
-// rows x 16 MT tokens over all of K), and wave w owns accumulator a = w: it
-// computes the terms of blocks 8c + w for c = 0, 1, ... in increasing order
-// and adds each to its accumulator as it goes, from +0.0f. The eight waves'
-// accumulators of an output then meet once, in the adjacent-pair tree.
+// Order. The contract's accumulator a (0..7) of an output adds the terms of
+// blocks a, a + 8, a + 16, ... in that order, and never sees another block. A
+// workgroup's eight waves share an item (16 rows x 16 MT tokens over all of
+// K), and wave w owns accumulator a = w: it computes the terms of blocks
+// 8c + w for c = 0, 1, ... in increasing order and adds each to its
+// accumulator as it goes, from +0.0f. At the item's end the eight waves'
+// accumulators of an output meet once, in the adjacent-pair tree.
 //
-// Data: each wave streams exactly the bytes it uses, straight from memory
-// into registers, D chunks ahead (D = 8 -- 4 for 64-token tiles -- or the
-// largest of 4, 2, 1 dividing the K / 256 chunks of a row, so that an item is
-// whole groups of D chunks
-// processed without a branch): per chunk, lane (row j, k-group g) loads the
-// dwords holding its 8-byte nibble run and scale of block 8c + w of row j
-// (the eight waves together read each 144-byte chunk once), and one 8-byte
-// piece of each token tile's activations. The activation scales of the
-// workgroup's tokens are staged in LDS once, block-major, so that the four
-// tokens an MFMA lane needs are one 16-byte read. Nothing else is shared, so
-// the waves meet only at item boundaries. Every load is a raw buffer load,
-// issued by every lane on every path: lanes with nothing to load (rows past
-// N, tokens past M, chunks past the workgroup's last item) are out of the
-// buffer's range and read nothing, so the waits on the loads in flight are
-// exact. Workgroups are persistent over items, and each wave's chunk stream
-// runs on across items.
+// Data. What bounds this path is the bytes in flight and how many cache lines
+// each load instruction touches, so every global load is a 16-byte piece of a
+// contiguous run, 1 KB per wave instruction:
+//  * A round is D consecutive chunks (8 D blocks, 256 D values of K) of one
+//    item: the 16 rows' D * 144 weight bytes, each a contiguous run in the
+//    ggml row, and the item's tokens' 256 D activation bytes and 8 D scales.
+//  * All 512 threads load a round's pieces into registers P rounds ahead of
+//    its use, and write it into one of two LDS round buffers once the round
+//    before has been computed. One barrier per round separates the writes of
+//    round q + 1 from the reads of round q - 1 in the same buffer.
+//  * Each wave then reads its MFMA operands from LDS: the weight dwords of
+//    block 8c + w of its row (realigned: a block starts every 18 bytes), one
+//    8-byte activation piece per token tile, and the four token scales of its
+//    output lanes as one 16-byte read (scales are stored block-major).
+//  * Loads and the output stores are raw buffer accesses issued by every
+//    thread in every round: lanes with nothing to move (rows past N, tokens
+//    past M, rounds past the workgroup's last) are out of the buffer's range
+//    and touch no memory. The number of memory operations in flight never
+//    depends on data, so the wait before each round's LDS write is exact: it
+//    waits for that round's loads only, with the next P - 1 rounds in flight.
+// Workgroups are persistent over items; a workgroup's rounds form one stream
+// that runs on across its items.
 #include "kernels.h"
 #include "q4_0_device.h"
 
@@ -50,10 +56,11 @@ namespace w4a8 {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GW = 8;                  // waves per workgroup; wave w owns accumulator w
 constexpr int GTHREADS = 64 * GW;
-constexpr int NR = 16;                 // the MFMA's 16 row columns
+constexpr int NR = 16;                 // rows per item: the MFMA's 16 row columns
 constexpr int OUT_OF_RANGE = 0x7ffffff0;
 constexpr uint32_t BUFFER_DWORD3 = 0x00020000;
 constexpr int CACHE_NT = 2;
@@ -65,6 +72,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, ui
 
 __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
+// DPP quad broadcast of lane R of each quad (quad_perm [R, R, R, R]). With
+// bound_ctrl set the compiler folds it into the consuming multiply as a DPP
+// source (v_mul_f32_dpp), so it costs no instruction of its own.
+template <int R>
+__device__ __forceinline__ float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), R * 0x55, 0xF, 0xF, true));
+}
+
 struct GemmParams {
     const uint8_t *w;
     const uint8_t *x;      // m rows, engine layout
@@ -75,171 +90,264 @@ struct GemmParams {
     int x_stride;          // bytes per activation row, k + k / 8
 };
 
-// LDS: activation scales [nb][16 MT] fp32, then two exchange buffers
-// [8][16 MT][NR] fp32 (consecutive items alternate between them).
-template <int MT>
-struct Lds {
-    static constexpr int EX_BYTES = GW * 16 * MT * NR * 4;
-    __host__ __device__ static int xd_bytes(int nb) { return nb * 16 * MT * 4; }
-    __host__ __device__ static int bytes(int nb) { return xd_bytes(nb) + 2 * EX_BYTES; }
+// Geometry of one instance: MT token tiles per item, D chunks per round, P
+// rounds in flight, OCC workgroups per CU (the LDS of one is then at most
+// LDS_MAX / OCC; with two, each SIMD runs four waves).
+template <int MT, int D, int P, int OCC>
+struct Geo {
+    static constexpr int TT = 16 * MT;                      // tokens per item
+    static constexpr int WP = D * CHUNK_BYTES + 16;         // LDS bytes per weight row (padded: bank spread)
+    static constexpr int AP = D * 256 + 16;                 // LDS bytes per token's int8 slice
+    static constexpr int W_OFF = 0;
+    static constexpr int X_OFF = NR * WP;
+    static constexpr int XD_OFF = X_OFF + TT * AP;          // fp32 scales [8 D blocks][TT tokens]
+    static constexpr int BUF = XD_OFF + 8 * D * TT * 4;     // one round
+    // Exchange of the eight accumulators: [8][TT][EXP] fp32. Two of them
+    // (consecutive items alternate) and a padded row pitch when they fit;
+    // with one, the workgroup meets once more after each item's reduction.
+    static constexpr int BUDGET = LDS_MAX / OCC;
+    static constexpr int ex_bytes(int pitch) { return GW * TT * pitch * 4; }
+    static constexpr int EXN = 2 * BUF + 2 * ex_bytes(NR) <= BUDGET ? 2 : 1;
+    static constexpr int EXP = 2 * BUF + EXN * ex_bytes(NR + 4) <= BUDGET ? NR + 4 : NR;
+    static constexpr int EX_BYTES = ex_bytes(EXP);
+    static constexpr int EX_OFF = 2 * BUF;
+    static constexpr int LDS = 2 * BUF + EXN * EX_BYTES;
+    static_assert(LDS <= BUDGET, "round buffers exceed the LDS budget");
+    static_assert(BUF < 65536, "a round buffer offset must fit an LDS instruction's immediate");
+    // 16-byte pieces of a round and the load slots per thread that carry them.
+    static constexpr int W_PIECES = NR * D * 9;
+    static constexpr int X_PIECES = TT * D * 16;
+    static constexpr int XD_PIECES = TT * D * 2;
+    static constexpr int SW = (W_PIECES + GTHREADS - 1) / GTHREADS;
+    static constexpr int SX = (X_PIECES + GTHREADS - 1) / GTHREADS;
+    static constexpr int SD = (XD_PIECES + GTHREADS - 1) / GTHREADS;
+    static constexpr int OUTS = (TT * NR + GTHREADS - 1) / GTHREADS;   // outputs per thread per item
 };
 
-// One chunk of one wave in registers.
-template <int MT>
-struct Chunk {
-    uint32_t w[4];           // the dwords holding the lane's nibble run, and its scale
-    uint32_t x[MT][2];       // the lane's 8 activation bytes of each token tile
+// One round's pieces in one thread's registers.
+template <int SW, int SX, int SD>
+struct Regs {
+    u32x4 w[SW];
+    u32x4 x[SX];
+    u32x4 d[SD];
 };
 
-template <int MT, int NRW, int D, bool ODD>
+template <int MT, int D, int P, int OCC, bool ODD>
 struct Kernel {
-    // Chunk c (block 8c + w of every row) of the item (n0, m0); live == false
-    // reads nothing.
-    static __device__ __forceinline__ void load(const GemmParams &P, int n0, int m0, int c, bool live, int row_bytes,
-                                                Chunk<MT> &ch) {
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        const int j = lane & 15, g = lane >> 4;
-        const int n = n0 + j;
-        const bool row_live = live && j < NRW && n < P.rows;
-        // Block 8c + w of row n starts at o = n * row_bytes + 18 (8c + w):
-        // even w at a dword boundary (the nibble run two bytes past it), odd
-        // w two bytes into a dword (the run dword-aligned, the scale in the
-        // high half of the dword before).
-        const int o = n * row_bytes + 18 * (8 * c + w);
-        const __amdgpu_buffer_rsrc_t wb = buffer_of(P.w, (uint32_t)((size_t)P.rows * row_bytes));
-        if constexpr (!ODD) {
-            const int base = row_live ? o + 8 * (g & 1) : OUT_OF_RANGE;
-            ch.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wb, base, 0, CACHE_NT);
-            ch.w[1] = __builtin_amdgcn_raw_buffer_load_b32(wb, base + 4, 0, CACHE_NT);
-            ch.w[2] = __builtin_amdgcn_raw_buffer_load_b32(wb, base + 8, 0, CACHE_NT);
-            ch.w[3] = __builtin_amdgcn_raw_buffer_load_b32(wb, row_live ? o : OUT_OF_RANGE, 0, CACHE_NT);
-        } else {
-            const int base = row_live ? o + 2 + 8 * (g & 1) : OUT_OF_RANGE;
-            ch.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wb, base, 0, CACHE_NT);
-            ch.w[1] = __builtin_amdgcn_raw_buffer_load_b32(wb, base + 4, 0, CACHE_NT);
-            ch.w[3] = __builtin_amdgcn_raw_buffer_load_b32(wb, row_live ? o - 2 : OUT_OF_RANGE, 0, CACHE_NT);
-        }
-        const __amdgpu_buffer_rsrc_t xb = buffer_of(P.x, (uint32_t)((size_t)P.m * P.x_stride));
+    using G = Geo<MT, D, P, OCC>;
+    using R = Regs<G::SW, G::SX, G::SD>;
+
+    // Per-thread offsets of its load slots and outputs, fixed for the whole
+    // launch. A round's loads go through buffer resources based at the
+    // round's first row / token and chunk, whose size is the bytes the round
+    // may read (zero for a dead round), so a lane's offset never changes and
+    // the resource alone bounds every access: a row past N or a token past M
+    // lies beyond the size. A slot with no piece has an offset beyond any size.
+    struct Slots {
+        uint32_t w_go[G::SW];
+        int w_lo[G::SW];       // LDS byte offset in a round buffer; -1 when the slot carries no piece
+        uint32_t x_go[G::SX];
+        int x_lo[G::SX];
+        uint32_t d_go[G::SD];
+        int d_lo[G::SD];       // LDS float index of the first of the piece's four scales
+        int o_ex[G::OUTS];     // exchange index of output o (accumulator 0)
+        int o_tok[G::OUTS];    // its token and row in the item; INT_MAX when none
+        int o_row[G::OUTS];
+        uint32_t o_y[G::OUTS]; // its byte offset from the item's first output
+    };
+
+    static __device__ __forceinline__ void slots(const GemmParams &Pm, int row_bytes, Slots &s) {
+        const int tid = threadIdx.x;
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int m = m0 + 16 * t + j;
-            const int off = live && m < P.m ? m * P.x_stride + 32 * (8 * c + w) + 8 * g : OUT_OF_RANGE;
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(xb, off, 0, 0);
-            ch.x[t][0] = (uint32_t)v[0];
-            ch.x[t][1] = (uint32_t)v[1];
+        for (int i = 0; i < G::SW; ++i) {
+            const int q = i * GTHREADS + tid;
+            const int r = q / (9 * D), p = q - r * (9 * D);
+            const bool has = q < G::W_PIECES;
+            s.w_go[i] = has ? (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.w_lo[i] = has ? G::W_OFF + r * G::WP + 16 * p : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i) {
+            const int q = i * GTHREADS + tid;
+            const int t = q / (16 * D), p = q - t * (16 * D);
+            const bool has = q < G::X_PIECES;
+            s.x_go[i] = has ? (uint32_t)t * (uint32_t)Pm.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.x_lo[i] = has ? G::X_OFF + t * G::AP + 16 * p : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i) {
+            // Tokens fastest, so that the transposing LDS writes hit distinct banks.
+            const int q = i * GTHREADS + tid;
+            const int p = q / G::TT, t = q - p * G::TT;
+            const bool has = q < G::XD_PIECES;
+            s.d_go[i] = has ? (uint32_t)t * (uint32_t)Pm.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.d_lo[i] = has ? G::XD_OFF / 4 + 4 * p * G::TT + t : -1;
+        }
+#pragma unroll
+        for (int o = 0; o < G::OUTS; ++o) {
+            const int idx = o * GTHREADS + tid;
+            const int tok = idx / NR, row = idx - tok * NR;
+            const bool has = idx < G::TT * NR;
+            s.o_ex[o] = tok * G::EXP + row;
+            s.o_tok[o] = has ? tok : 0x7fffffff;
+            s.o_row[o] = row;
+            s.o_y[o] = ((uint32_t)tok * (uint32_t)Pm.rows + (uint32_t)row) * 4u;
         }
     }
 
-    // The terms of block 8c + w, added to the wave's accumulators.
-    static __device__ __forceinline__ void compute(const Chunk<MT> &ch, const float *xd, int c, float acc[MT][4]) {
+    // Issue the loads of one round: rows n0.. (rows_left of them before the
+    // end of W), tokens m0.. (toks_left), chunks c0 .. c0 + D - 1. The last
+    // row a round may read ends at byte (rows_left - 1) row_bytes + 144 (c0 + D)
+    // <= rows_left row_bytes - 144 c0 from the round's base, the next row
+    // starts past that; likewise for the tokens' int8 (256 D of each
+    // x_stride = K + K/8 bytes) and scales (32 D, after K).
+    static __device__ __forceinline__ void load(const GemmParams &Pm, const Slots &s, int row_bytes, int n0, int m0,
+                                                int c0, bool live, R &rg) {
+        const uint32_t rows_left = (uint32_t)(Pm.rows - n0), toks_left = (uint32_t)(Pm.m - m0);
+        const uint8_t *wbase = Pm.w + (size_t)n0 * row_bytes + (size_t)c0 * CHUNK_BYTES;
+        const uint8_t *xrow = Pm.x + (size_t)m0 * Pm.x_stride;
+        const __amdgpu_buffer_rsrc_t wb =
+            buffer_of(wbase, live ? rows_left * (uint32_t)row_bytes - (uint32_t)c0 * CHUNK_BYTES : 0u);
+        const __amdgpu_buffer_rsrc_t xb =
+            buffer_of(xrow + (size_t)c0 * 256, live ? toks_left * (uint32_t)Pm.x_stride - (uint32_t)c0 * 256u : 0u);
+        const __amdgpu_buffer_rsrc_t db =
+            buffer_of(xrow + Pm.k + (size_t)c0 * 32,
+                      live ? toks_left * (uint32_t)Pm.x_stride - (uint32_t)Pm.k - (uint32_t)c0 * 32u : 0u);
+#pragma unroll
+        for (int i = 0; i < G::SW; ++i) rg.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wb, (int)s.w_go[i], 0, CACHE_NT);
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i) rg.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xb, (int)s.x_go[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i) rg.d[i] = __builtin_amdgcn_raw_buffer_load_b128(db, (int)s.d_go[i], 0, 0);
+    }
+
+    // Write one round from registers into an LDS round buffer.
+    static __device__ __forceinline__ void stage(uint8_t *buf, const Slots &s, const R &rg) {
+#pragma unroll
+        for (int i = 0; i < G::SW; ++i)
+            if ((i + 1) * GTHREADS <= G::W_PIECES || s.w_lo[i] >= 0)
+                *reinterpret_cast<u32x4 *>(buf + s.w_lo[i]) = rg.w[i];
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i)
+            if ((i + 1) * GTHREADS <= G::X_PIECES || s.x_lo[i] >= 0)
+                *reinterpret_cast<u32x4 *>(buf + s.x_lo[i]) = rg.x[i];
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i)
+            if ((i + 1) * GTHREADS <= G::XD_PIECES || s.d_lo[i] >= 0) {
+                uint32_t *xd = reinterpret_cast<uint32_t *>(buf) + s.d_lo[i];
+                const u32x4 v = rg.d[i];
+                xd[0] = v.x;
+                xd[G::TT] = v.y;
+                xd[2 * G::TT] = v.z;
+                xd[3 * G::TT] = v.w;
+            }
+    }
+
+    // The terms of blocks 8c + w (c = 0..D-1) of one round, added in order to
+    // the wave's accumulators.
+    static __device__ __forceinline__ void compute(const uint8_t *buf, float acc[MT][4]) {
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        const int g = lane >> 4;
+        const int j = lane & 15, g = lane >> 4;
+        const int h = g & 1;
         const int shift = (g >> 1) * 4;
-        uint32_t lo, hi, d_bits;
-        if constexpr (!ODD) {
-            lo = __builtin_amdgcn_alignbyte(ch.w[1], ch.w[0], 2);
-            hi = __builtin_amdgcn_alignbyte(ch.w[2], ch.w[1], 2);
-            d_bits = ch.w[3] & 0xFFFFu;                    // the low half of the block's first dword
-        } else {
-            lo = ch.w[0];
-            hi = ch.w[1];
-            d_bits = ch.w[3] >> 16;                        // the high half of the dword before the run
-        }
-        const long bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
         const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
-        const float dw = half_bits_to_float(d_bits);
-        const int b = 8 * c + w;
+        // Block 8c + w of row j starts at byte 18 w of its chunk: an even w at
+        // a dword boundary (scale in the low half, the nibble run two bytes
+        // in), an odd w two bytes into a dword (scale in the high half of the
+        // dword before, the run dword-aligned). This lane's run is nibble
+        // bytes 8h .. 8h + 7. Every address below is one dword-aligned base
+        // plus constant offsets.
+        const uint8_t *wrow = buf + G::W_OFF + j * G::WP + 18 * w;
+        const uint32_t *run = reinterpret_cast<const uint32_t *>(wrow + (ODD ? 2 : 0) + 8 * h);
+        const uint32_t *scl = reinterpret_cast<const uint32_t *>(wrow - (ODD ? 2 : 0));
+        const uint8_t *xa = buf + G::X_OFF + j * G::AP + 32 * w + 8 * g;
+        // The lane reads the scale of token 4g + (j & 3) of its tile; the
+        // four lanes of a quad then hold the scales of the four tokens of the
+        // lane's outputs, and a DPP quad broadcast hands scale r to output r.
+        const float *xs = reinterpret_cast<const float *>(buf + G::XD_OFF) + w * G::TT + 4 * g + (j & 3);
+        // Phase 1: the integer block sums of the whole round (independent, so
+        // the MFMAs issue back to back while the next operands are read).
+        v4i v[D][MT];
+        float dw[D], dx[D][MT];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            v4i v = {0, 0, 0, 0};
-            const long ax = as_long(ch.x[t][0], ch.x[t][1]);
-            v = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, v, 0, 0, 0);
-            v = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, v, 0, 0, 0);
-            const float4 dx = *reinterpret_cast<const float4 *>(xd + b * 16 * MT + 16 * t + 4 * g);
-            const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+        for (int c = 0; c < D; ++c) {
+            uint32_t lo, hi, d_bits;
+            if constexpr (!ODD) {
+                const uint32_t v0 = run[36 * c], v1 = run[36 * c + 1], v2 = run[36 * c + 2];
+                lo = __builtin_amdgcn_alignbyte(v1, v0, 2);
+                hi = __builtin_amdgcn_alignbyte(v2, v1, 2);
+                d_bits = scl[36 * c] & 0xFFFFu;
+            } else {
+                lo = run[36 * c];
+                hi = run[36 * c + 1];
+                d_bits = scl[36 * c] >> 16;
+            }
+            const long bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
+            dw[c] = half_bits_to_float(d_bits);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float a = (float)v[r] * dw;
-                acc[t][r] = acc[t][r] + a * dxs[r];
+            for (int t = 0; t < MT; ++t) {
+                const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::AP + 256 * c);
+                dx[c][t] = xs[8 * c * G::TT + 16 * t];
+                v4i z = {0, 0, 0, 0};
+                z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+                v[c][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
             }
         }
-    }
-
-    // Activation scales of tokens m0 .. m0 + 16 MT - 1, block-major, into LDS.
-    static __device__ __forceinline__ void stage_scales(const GemmParams &P, int m0, int nb, float *xd) {
-        const __amdgpu_buffer_rsrc_t xb = buffer_of(P.x, (uint32_t)((size_t)P.m * P.x_stride));
-        const int per_tok = nb / 4;                          // four blocks of one token per piece
-        for (int p = threadIdx.x; p < 16 * MT * per_tok; p += GTHREADS) {
-            const int tok = p / per_tok, b4 = 4 * (p - tok * per_tok);
-            const int m = m0 + tok;
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-                xb, m < P.m ? m * P.x_stride + P.k + 4 * b4 : OUT_OF_RANGE, 0, 0);
+        // Phase 2: the fp32 terms, added to each accumulator in block order.
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xd[(b4 + e) * 16 * MT + tok] = __uint_as_float((uint32_t)v[e]);
-        }
+        for (int c = 0; c < D; ++c)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const float dxs[4] = {quad_bcast<0>(dx[c][t]), quad_bcast<1>(dx[c][t]), quad_bcast<2>(dx[c][t]),
+                                      quad_bcast<3>(dx[c][t])};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a = (float)v[c][t][r] * dw[c];
+                    acc[t][r] = acc[t][r] + a * dxs[r];
+                }
+            }
     }
 
-    // The eight accumulators of each output of the item (n0, m0) meet in the
-    // adjacent-pair tree; the registers then restart from +0.0f.
-    static __device__ __forceinline__ void finish(const GemmParams &P, float *ex, int n0, int m0, float acc[MT][4]) {
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    static __device__ __forceinline__ void run(const GemmParams &Pm, uint8_t *lds) {
+        const int tid = threadIdx.x;
+        const int lane = tid & 63, w = tid >> 6;
         const int j = lane & 15, g = lane >> 4;
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ex[(w * 16 * MT + 16 * t + 4 * g + r) * NR + j] = acc[t][r];
-                acc[t][r] = 0.0f;
-            }
-        __syncthreads();
-        for (int o = threadIdx.x; o < 16 * MT * NRW; o += GTHREADS) {
-            const int tok = o / NRW, j2 = o - tok * NRW;
-            float l[8];
-#pragma unroll
-            for (int a = 0; a < 8; ++a) l[a] = ex[(a * 16 * MT + tok) * NR + j2];
-            const float yv = ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]));
-            const int m = m0 + tok, n = n0 + j2;
-            if (m < P.m && n < P.rows) P.y[(size_t)m * P.rows + n] = yv;
-        }
-    }
+        const int C = Pm.k >> 8;
+        const int RPI = C / D;                                  // rounds per item (D divides C)
+        const int row_bytes = C * CHUNK_BYTES;
+        const int n_rt = (Pm.rows + NR - 1) / NR;
+        const int items = n_rt * ((Pm.m + G::TT - 1) / G::TT);
+        const int GD = gridDim.x;
+        const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / GD + 1 : 0;
+        const int Q = my_items * RPI;                           // rounds of this workgroup
+        const int QP = (Q + P - 1) / P * P;                     // padded to whole groups of P
 
-    static __device__ __forceinline__ void run(const GemmParams &P, uint8_t *lds) {
-        const int nb = P.k >> 5;
-        const int C = nb >> 3;                                  // chunks per row = blocks per wave per item
-        const int row_bytes = nb * Q4_0_BYTES;
-        const int n_rt = (P.rows + NRW - 1) / NRW;
-        const int items = n_rt * ((P.m + 16 * MT - 1) / (16 * MT));
-        const int G = gridDim.x;
-        const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / G + 1 : 0;
-        const int S = my_items * C;                             // chunks in each wave's stream
-        float *xd = reinterpret_cast<float *>(lds);
-        float *ex0 = reinterpret_cast<float *>(lds + Lds<MT>::xd_bytes(nb));
-        float *ex1 = ex0 + Lds<MT>::EX_BYTES / 4;
+        Slots s;
+        slots(Pm, row_bytes, s);
 
-        auto item_of = [&](int k, int &n0, int &m0) {
-            const int it = (int)blockIdx.x + k * G;
+        // Round q of the stream: item q / RPI, chunks (q % RPI) D ..
+        auto geo = [&](int q, int &n0, int &m0, int &c0, int &kk) {
+            const bool live = q < Q;
+            kk = live ? q / RPI : 0;
+            c0 = live ? (q - kk * RPI) * D : 0;
+            const int it = (int)blockIdx.x + kk * GD;
             const int tg = it / n_rt;
-            n0 = (it - tg * n_rt) * NRW;
-            m0 = tg * 16 * MT;
+            n0 = (it - tg * n_rt) * NR;
+            m0 = tg * G::TT;
+            return live;
         };
-        auto load_q = [&](int q, Chunk<MT> &ch) {
-            const bool live = q < S;
-            const int k = live ? q / C : 0;
-            int n0, m0;
-            item_of(k, n0, m0);
-            load(P, n0, m0, live ? q - k * C : 0, live, row_bytes, ch);
+        auto load_q = [&](int q, R &rg) {
+            int n0, m0, c0, kk;
+            const bool live = geo(q, n0, m0, c0, kk);
+            load(Pm, s, row_bytes, n0, m0, c0, live, rg);
         };
+        const size_t y_total = (size_t)Pm.m * Pm.rows * 4;
 
-        // The first item's token group: scales staged before anything else.
-        int cur_m0 = 0;
-        {
-            int n0;
-            item_of(0, n0, cur_m0);
-            if (my_items > 0) stage_scales(P, cur_m0, nb, xd);
-        }
-        Chunk<MT> st[D];
+        R rg[P];
 #pragma unroll
-        for (int d = 0; d < D; ++d) load_q(d, st[d]);
+        for (int d = 0; d < P; ++d) load_q(d, rg[d]);
+        stage(lds, s, rg[0]);
+        load_q(P, rg[0]);
         __syncthreads();
 
         float acc[MT][4];
@@ -248,44 +356,75 @@ struct Kernel {
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
 
-        // Each item is C / D groups of D chunks; stage d holds chunk q0 + d
-        // of the stream and is refilled with chunk q0 + D + d after the
-        // group, so the loads run one group ahead and a group is straight-
-        // line code.
-        int q0 = 0;
-        for (int k = 0; k < my_items; ++k) {
-            int n0, m0;
-            item_of(k, n0, m0);
-            if (m0 != cur_m0) {                                 // a new token group (M > 16 MT)
-                __syncthreads();
-                stage_scales(P, m0, nb, xd);
-                __syncthreads();
-                cur_m0 = m0;
-            }
-            for (int c0 = 0; c0 < C; c0 += D, q0 += D) {
+        for (int q0 = 0; q0 < QP; q0 += P) {
 #pragma unroll
-                for (int d = 0; d < D; ++d) compute(st[d], xd, c0 + d, acc);
+            for (int d = 0; d < P; ++d) {
+                const int q = q0 + d;
+                int n0, m0, c0, kk;
+                const bool live = geo(q, n0, m0, c0, kk);
+                const bool item_end = live && c0 + D == C;
+                float *ex = reinterpret_cast<float *>(lds + G::EX_OFF + (G::EXN == 2 ? (kk & 1) * G::EX_BYTES : 0));
+                if (live) compute(lds + (q & 1) * G::BUF, acc);
+                if (item_end) {
 #pragma unroll
-                for (int d = 0; d < D; ++d) load_q(q0 + D + d, st[d]);
+                    for (int t = 0; t < MT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            ex[(w * G::TT + 16 * t + 4 * g + r) * G::EXP + j] = acc[t][r];
+                            acc[t][r] = 0.0f;
+                        }
+                }
+                // Round q + 1 into the other buffer (last read by round q - 1,
+                // before the previous barrier), then its registers take round
+                // q + 1 + P.
+                stage(lds + ((q + 1) & 1) * G::BUF, s, rg[(d + 1) % P]);
+                load_q(q + 1 + P, rg[(d + 1) % P]);
+                __syncthreads();
+                // At an item's end: the eight accumulators of each output meet
+                // in the adjacent-pair tree. Every thread issues its stores in
+                // every round; the resource is empty when there is nothing to
+                // store, and a lane past M or N stores out of range.
+                const size_t y0 = ((size_t)m0 * Pm.rows + n0) * 4;
+                const __amdgpu_buffer_rsrc_t yb =
+                    buffer_of(reinterpret_cast<uint8_t *>(Pm.y) + y0, item_end ? (uint32_t)(y_total - y0) : 0u);
+#pragma unroll
+                for (int o = 0; o < G::OUTS; ++o) {
+                    float yv = 0.0f;
+                    if (item_end && s.o_tok[o] < G::TT) {
+                        float l[8];
+#pragma unroll
+                        for (int a = 0; a < 8; ++a) l[a] = ex[a * G::TT * G::EXP + s.o_ex[o]];
+                        yv = ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]));
+                    }
+                    const bool ok = s.o_tok[o] < Pm.m - m0 && s.o_row[o] < Pm.rows - n0;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), yb, ok ? (int)s.o_y[o] : OUT_OF_RANGE,
+                                                          0, 0);
+                }
+                if (G::EXN == 1 && item_end) __syncthreads();   // the exchange is read before it is written again
             }
-            finish(P, (k & 1) ? ex1 : ex0, n0, m0, acc);
         }
     }
 };
 
-template <int MT, int NRW, int D>
-__global__ __launch_bounds__(GTHREADS) void gemm_mfma_kernel(GemmParams P) {
+template <int MT, int D, int P, int OCC>
+__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(2 * OCC, 2 * OCC)))
+void gemm_mfma_kernel(GemmParams Pm) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if ((threadIdx.x >> 6) & 1)
-        Kernel<MT, NRW, D, true>::run(P, lds);
+        Kernel<MT, D, P, OCC, true>::run(Pm, lds);
     else
-        Kernel<MT, NRW, D, false>::run(P, lds);
+        Kernel<MT, D, P, OCC, false>::run(Pm, lds);
 }
 
-template <int MT, int NRW, int D>
-hipError_t launch_mt(const GemmParams &P, hipStream_t stream) {
-    const void *fn = reinterpret_cast<const void *>(&gemm_mfma_kernel<MT, NRW, D>);
-    const int lds = Lds<MT>::bytes(P.k / QK);
+#ifndef W4A8_GEMM_DEPTH
+#define W4A8_GEMM_DEPTH 2
+#endif
+constexpr int DEPTH = W4A8_GEMM_DEPTH;
+
+template <int MT, int D, int OCC>
+hipError_t launch_geo(const GemmParams &Pm, hipStream_t stream) {
+    using G = Geo<MT, D, DEPTH, OCC>;
+    const void *fn = reinterpret_cast<const void *>(&gemm_mfma_kernel<MT, D, DEPTH, OCC>);
     static bool lds_allowed = false;
     if (!lds_allowed) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_MAX);
@@ -293,56 +432,71 @@ hipError_t launch_mt(const GemmParams &P, hipStream_t stream) {
         lds_allowed = true;
     }
     int per_cu = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, lds);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, G::LDS);
     if (e != hipSuccess) return e;
     if (per_cu < 1) per_cu = 1;
-    const long items = (long)((P.rows + NRW - 1) / NRW) * ((P.m + 16 * MT - 1) / (16 * MT));
+    const long items = (long)((Pm.rows + NR - 1) / NR) * ((Pm.m + G::TT - 1) / G::TT);
     long grid = (long)device_cu_count() * per_cu;
     if (grid > items) grid = items;
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, NRW, D>), dim3((unsigned)grid), dim3(GTHREADS), lds, stream, P);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, D, DEPTH, OCC>), dim3((unsigned)grid), dim3(GTHREADS), G::LDS, stream, Pm);
     return hipGetLastError();
 }
 
-template <int MT, int NRW>
-hipError_t launch_depth(const GemmParams &P, hipStream_t stream) {
-    const int C = P.k / 256;
-    if constexpr (MT < 4) {                 // a 64-token tile's stages only fit four deep
-        if (C % 8 == 0) return launch_mt<MT, NRW, 8>(P, stream);
+// Chunks per round: the largest power of two up to DMAX that divides the
+// K / 256 chunks of a row, so that every item is whole rounds.
+template <int MT, int DMAX, int OCC>
+hipError_t launch_mt(const GemmParams &Pm, hipStream_t stream) {
+    const int C = Pm.k / 256;
+    if constexpr (DMAX >= 8) {
+        if (C % 8 == 0) return launch_geo<MT, 8, OCC>(Pm, stream);
     }
-    if (C % 4 == 0) return launch_mt<MT, NRW, 4>(P, stream);
-    if (C % 2 == 0) return launch_mt<MT, NRW, 2>(P, stream);
-    return launch_mt<MT, NRW, 1>(P, stream);
+    if constexpr (DMAX >= 4) {
+        if (C % 4 == 0) return launch_geo<MT, 4, OCC>(Pm, stream);
+    }
+    if constexpr (DMAX >= 2) {
+        if (C % 2 == 0) return launch_geo<MT, 2, OCC>(Pm, stream);
+    }
+    return launch_geo<MT, 1, OCC>(Pm, stream);
 }
 
-template <int MT>
-hipError_t launch_rows(const GemmParams &P, hipStream_t stream) {
-    // 16-row items unless that leaves fewer items than two per CU.
-    const long items16 = (long)((P.rows + 15) / 16) * ((P.m + 16 * MT - 1) / (16 * MT));
-    return items16 >= 2L * device_cu_count() ? launch_depth<MT, 16>(P, stream) : launch_depth<MT, 8>(P, stream);
+#ifndef W4A8_GEMM_OCC
+#define W4A8_GEMM_OCC 2
+#endif
+
+hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
+    // 16, 32 or 64 tokens per item (all of M up to 64, so the weights stream
+    // once); a round holds 128 (or, at two workgroups per CU, 64) token-chunks
+    // of activations.
+    constexpr int OCC = W4A8_GEMM_OCC;
+    if (Pm.m <= 16) return launch_mt<1, 8 / OCC, OCC>(Pm, stream);
+    if (Pm.m <= 32) return launch_mt<2, 4 / OCC, OCC>(Pm, stream);
+    return launch_mt<4, 2 / OCC, OCC>(Pm, stream);
 }
 
 }  // namespace
 
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hipStream_t stream) {
+    // One token is the M = 1 GEMV, byte for byte by the contract, and faster.
+    if (m == 1) return launch_gemv_m1(w, x, X_ENGINE, y, stream);
     GemmParams P{};
     P.w = w.seg[0];
-    P.x = x;
-    P.y = y;
     P.rows = w.rows;
     P.k = w.k;
-    P.m = m;
     P.x_stride = w.k + w.k / 8;
-    // Buffer ranges are 32-bit byte counts.
-    if ((size_t)P.rows * (size_t)(P.k / QK * Q4_0_BYTES) >= 0x7fff0000u ||
-        (size_t)P.m * (size_t)P.x_stride >= 0x7fff0000u)
-        return hipErrorInvalidValue;
-    // Token tiles per workgroup: all of M up to 64 tokens, so the weights
-    // stream once; beyond that, groups of 64 (32 when K is so long that a
-    // group's activation scales would not fit in LDS).
-    const int nb = P.k / QK;
-    if (m <= 16) return launch_rows<1>(P, stream);
-    if (m <= 32 || Lds<4>::bytes(nb) > LDS_MAX) return launch_rows<2>(P, stream);
-    return launch_rows<4>(P, stream);
+    // Buffer ranges are 32-bit byte counts: the weights must fit one, and the
+    // tokens go in launches whose activations and outputs each fit one.
+    if ((size_t)P.rows * (size_t)(P.k / QK * Q4_0_BYTES) >= 0x7fff0000u) return hipErrorInvalidValue;
+    const size_t per_token = (size_t)P.x_stride > (size_t)P.rows * 4 ? (size_t)P.x_stride : (size_t)P.rows * 4;
+    int group = (int)(0x7fff0000u / per_token) / 64 * 64;
+    if (group < 64) return hipErrorInvalidValue;
+    for (int m0 = 0; m0 < m; m0 += group) {
+        P.x = x + (size_t)m0 * P.x_stride;
+        P.y = y + (size_t)m0 * P.rows;
+        P.m = m - m0 < group ? m - m0 : group;
+        const hipError_t e = launch_tokens(P, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace w4a8

@@ -207,7 +207,10 @@ def test_gemv_quarters_at_separate_addresses(gpu):
 # ------------------------------------------------------------------ gemm
 
 @pytest.mark.parametrize("m,rows,k", [(2, 64, 2048), (4, 100, 512), (16, 256, 2048), (17, 48, 8192),
-                                      (24, 512, 2048), (33, 80, 1024), (64, 128, 2048)])
+                                      (24, 512, 2048), (33, 80, 1024), (64, 128, 2048),
+                                      # one chunk per row; three and five chunks (rounds of one chunk);
+                                      # several 64-token groups; one row
+                                      (8, 16, 256), (40, 33, 768), (130, 40, 1280), (2, 1, 512)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
