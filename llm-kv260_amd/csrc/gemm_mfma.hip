@@ -100,8 +100,12 @@ struct Geo {
     static constexpr int AP = D * 256 + 16;                 // LDS bytes per token's int8 slice
     static constexpr int W_OFF = 0;
     static constexpr int X_OFF = NR * WP;
-    static constexpr int XD_OFF = X_OFF + TT * AP;          // fp32 scales [8 D blocks][TT tokens]
-    static constexpr int BUF = XD_OFF + 8 * D * TT * 4;     // one round
+    // fp32 scales [8 D blocks][XDP], tokens along a row. The pitch makes the
+    // transposing writes (64 / TT pieces of consecutive tokens per wave
+    // instruction, four rows apart) fall in distinct banks.
+    static constexpr int XDP = TT < 64 ? TT + TT / 4 : TT;
+    static constexpr int XD_OFF = X_OFF + TT * AP;
+    static constexpr int BUF = XD_OFF + 8 * D * XDP * 4;    // one round
     // Exchange of the eight accumulators: [8][TT][EXP] fp32. Two of them
     // (consecutive items alternate) and a padded row pitch when they fit;
     // with one, the workgroup meets once more after each item's reduction.
@@ -181,7 +185,7 @@ struct Kernel {
             const int p = q / G::TT, t = q - p * G::TT;
             const bool has = q < G::XD_PIECES;
             s.d_go[i] = has ? (uint32_t)t * (uint32_t)Pm.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
-            s.d_lo[i] = has ? G::XD_OFF / 4 + 4 * p * G::TT + t : -1;
+            s.d_lo[i] = has ? G::XD_OFF / 4 + 4 * p * G::XDP + t : -1;
         }
 #pragma unroll
         for (int o = 0; o < G::OUTS; ++o) {
@@ -237,9 +241,9 @@ struct Kernel {
                 uint32_t *xd = reinterpret_cast<uint32_t *>(buf) + s.d_lo[i];
                 const u32x4 v = rg.d[i];
                 xd[0] = v.x;
-                xd[G::TT] = v.y;
-                xd[2 * G::TT] = v.z;
-                xd[3 * G::TT] = v.w;
+                xd[G::XDP] = v.y;
+                xd[2 * G::XDP] = v.z;
+                xd[3 * G::XDP] = v.w;
             }
     }
 
@@ -264,7 +268,7 @@ struct Kernel {
         // The lane reads the scale of token 4g + (j & 3) of its tile; the
         // four lanes of a quad then hold the scales of the four tokens of the
         // lane's outputs, and a DPP quad broadcast hands scale r to output r.
-        const float *xs = reinterpret_cast<const float *>(buf + G::XD_OFF) + w * G::TT + 4 * g + (j & 3);
+        const float *xs = reinterpret_cast<const float *>(buf + G::XD_OFF) + w * G::XDP + 4 * g + (j & 3);
         // Phase 1: the integer block sums of the whole round (independent, so
         // the MFMAs issue back to back while the next operands are read).
         v4i v[D][MT];
@@ -287,7 +291,7 @@ struct Kernel {
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::AP + 256 * c);
-                dx[c][t] = xs[8 * c * G::TT + 16 * t];
+                dx[c][t] = xs[8 * c * G::XDP + 16 * t];
                 v4i z = {0, 0, 0, 0};
                 z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
                 v[c][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
@@ -308,6 +312,11 @@ struct Kernel {
             }
     }
 
+    // The workgroup's rounds form one stream over its items (row tiles
+    // blockIdx.x, blockIdx.x + gridDim.x, ...; a launch covers one group of at
+    // most TT tokens): round q is round q % RPI of item q / RPI. Two positions
+    // walk the stream, the round being computed and the round being loaded
+    // (P + 1 ahead), each advanced by one per round without a division.
     static __device__ __forceinline__ void run(const GemmParams &Pm, uint8_t *lds) {
         const int tid = threadIdx.x;
         const int lane = tid & 63, w = tid >> 6;
@@ -315,39 +324,32 @@ struct Kernel {
         const int C = Pm.k >> 8;
         const int RPI = C / D;                                  // rounds per item (D divides C)
         const int row_bytes = C * CHUNK_BYTES;
-        const int n_rt = (Pm.rows + NR - 1) / NR;
-        const int items = n_rt * ((Pm.m + G::TT - 1) / G::TT);
+        const int items = (Pm.rows + NR - 1) / NR;
         const int GD = gridDim.x;
         const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / GD + 1 : 0;
-        const int Q = my_items * RPI;                           // rounds of this workgroup
-        const int QP = (Q + P - 1) / P * P;                     // padded to whole groups of P
+        const int QP = (my_items * RPI + P - 1) / P * P;        // rounds, padded to whole groups of P
 
         Slots s;
         slots(Pm, row_bytes, s);
 
-        // Round q of the stream: item q / RPI, chunks (q % RPI) D ..
-        auto geo = [&](int q, int &n0, int &m0, int &c0, int &kk) {
-            const bool live = q < Q;
-            kk = live ? q / RPI : 0;
-            c0 = live ? (q - kk * RPI) * D : 0;
-            const int it = (int)blockIdx.x + kk * GD;
-            const int tg = it / n_rt;
-            n0 = (it - tg * n_rt) * NR;
-            m0 = tg * G::TT;
-            return live;
+        auto load_at = [&](int kk, int ss, R &rg) {
+            load(Pm, s, row_bytes, ((int)blockIdx.x + kk * GD) * NR, 0, ss * D, kk < my_items, rg);
         };
-        auto load_q = [&](int q, R &rg) {
-            int n0, m0, c0, kk;
-            const bool live = geo(q, n0, m0, c0, kk);
-            load(Pm, s, row_bytes, n0, m0, c0, live, rg);
+        auto advance = [&](int &kk, int &ss) {
+            if (++ss == RPI) {
+                ss = 0;
+                ++kk;
+            }
         };
-        const size_t y_total = (size_t)Pm.m * Pm.rows * 4;
+        const uint32_t y_total = (uint32_t)((size_t)Pm.m * Pm.rows * 4);
 
         R rg[P];
 #pragma unroll
-        for (int d = 0; d < P; ++d) load_q(d, rg[d]);
+        for (int d = 0; d < P; ++d) load_at(d / RPI, d % RPI, rg[d]);
         stage(lds, s, rg[0]);
-        load_q(P, rg[0]);
+        int lk = P / RPI, ls = P % RPI;                         // the load position: round P
+        load_at(lk, ls, rg[0]);
+        advance(lk, ls);
         __syncthreads();
 
         float acc[MT][4];
@@ -356,14 +358,15 @@ struct Kernel {
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
 
+        int ck = 0, cs = 0;                                     // the compute position: round q
         for (int q0 = 0; q0 < QP; q0 += P) {
 #pragma unroll
             for (int d = 0; d < P; ++d) {
                 const int q = q0 + d;
-                int n0, m0, c0, kk;
-                const bool live = geo(q, n0, m0, c0, kk);
-                const bool item_end = live && c0 + D == C;
-                float *ex = reinterpret_cast<float *>(lds + G::EX_OFF + (G::EXN == 2 ? (kk & 1) * G::EX_BYTES : 0));
+                const bool live = ck < my_items;
+                const bool item_end = live && cs == RPI - 1;
+                const int n0 = ((int)blockIdx.x + ck * GD) * NR;
+                float *ex = reinterpret_cast<float *>(lds + G::EX_OFF + (G::EXN == 2 ? (ck & 1) * G::EX_BYTES : 0));
                 if (live) compute(lds + (q & 1) * G::BUF, acc);
                 if (item_end) {
 #pragma unroll
@@ -378,15 +381,16 @@ struct Kernel {
                 // before the previous barrier), then its registers take round
                 // q + 1 + P.
                 stage(lds + ((q + 1) & 1) * G::BUF, s, rg[(d + 1) % P]);
-                load_q(q + 1 + P, rg[(d + 1) % P]);
+                load_at(lk, ls, rg[(d + 1) % P]);
+                advance(lk, ls);
                 __syncthreads();
                 // At an item's end: the eight accumulators of each output meet
                 // in the adjacent-pair tree. Every thread issues its stores in
                 // every round; the resource is empty when there is nothing to
                 // store, and a lane past M or N stores out of range.
-                const size_t y0 = ((size_t)m0 * Pm.rows + n0) * 4;
+                const uint32_t y0 = (uint32_t)n0 * 4u;
                 const __amdgpu_buffer_rsrc_t yb =
-                    buffer_of(reinterpret_cast<uint8_t *>(Pm.y) + y0, item_end ? (uint32_t)(y_total - y0) : 0u);
+                    buffer_of(reinterpret_cast<uint8_t *>(Pm.y) + y0, item_end ? y_total - y0 : 0u);
 #pragma unroll
                 for (int o = 0; o < G::OUTS; ++o) {
                     float yv = 0.0f;
@@ -396,11 +400,12 @@ struct Kernel {
                         for (int a = 0; a < 8; ++a) l[a] = ex[a * G::TT * G::EXP + s.o_ex[o]];
                         yv = ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]));
                     }
-                    const bool ok = s.o_tok[o] < Pm.m - m0 && s.o_row[o] < Pm.rows - n0;
+                    const bool ok = s.o_tok[o] < Pm.m && s.o_row[o] < Pm.rows - n0;
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), yb, ok ? (int)s.o_y[o] : OUT_OF_RANGE,
                                                           0, 0);
                 }
                 if (G::EXN == 1 && item_end) __syncthreads();   // the exchange is read before it is written again
+                advance(ck, cs);
             }
         }
     }
@@ -435,7 +440,7 @@ hipError_t launch_geo(const GemmParams &Pm, hipStream_t stream) {
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, G::LDS);
     if (e != hipSuccess) return e;
     if (per_cu < 1) per_cu = 1;
-    const long items = (long)((Pm.rows + NR - 1) / NR) * ((Pm.m + G::TT - 1) / G::TT);
+    const long items = (Pm.rows + NR - 1) / NR;
     long grid = (long)device_cu_count() * per_cu;
     if (grid > items) grid = items;
     hipLaunchKernelGGL((gemm_mfma_kernel<MT, D, DEPTH, OCC>), dim3((unsigned)grid), dim3(GTHREADS), G::LDS, stream, Pm);
@@ -483,16 +488,16 @@ hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hi
     P.rows = w.rows;
     P.k = w.k;
     P.x_stride = w.k + w.k / 8;
-    // Buffer ranges are 32-bit byte counts: the weights must fit one, and the
-    // tokens go in launches whose activations and outputs each fit one.
-    if ((size_t)P.rows * (size_t)(P.k / QK * Q4_0_BYTES) >= 0x7fff0000u) return hipErrorInvalidValue;
-    const size_t per_token = (size_t)P.x_stride > (size_t)P.rows * 4 ? (size_t)P.x_stride : (size_t)P.rows * 4;
-    int group = (int)(0x7fff0000u / per_token) / 64 * 64;
-    if (group < 64) return hipErrorInvalidValue;
-    for (int m0 = 0; m0 < m; m0 += group) {
+    // Buffer ranges are 32-bit byte counts: the weights must fit one. Tokens
+    // go in launches of at most 64 (one item's tokens, so the weights stream
+    // once per launch), whose activations and outputs then fit one too.
+    if ((size_t)P.rows * (size_t)(P.k / QK * Q4_0_BYTES) >= 0x7fff0000u ||
+        (size_t)64 * P.rows * 4 >= 0x7fff0000u)
+        return hipErrorInvalidValue;
+    for (int m0 = 0; m0 < m; m0 += 64) {
         P.x = x + (size_t)m0 * P.x_stride;
         P.y = y + (size_t)m0 * P.rows;
-        P.m = m - m0 < group ? m - m0 : group;
+        P.m = m - m0 < 64 ? m - m0 : 64;
         const hipError_t e = launch_tokens(P, stream);
         if (e != hipSuccess) return e;
     }
