@@ -21,6 +21,11 @@ Prints one JSON line. Besides the chain (value), it reports:
   gemv         microseconds per GEMV at every shape, weights rotated past the
                Infinity Cache, launched back to back from a HIP graph
   gemm         the M > 1 sweep (M = 1 .. 64) at gate|up and down
+  caller       the reference's decode-side caller (engine_t of
+               board/tp/tp_llama.cpp, rebuilt against the reference driver
+               headers: llm-kv260_amd/caller/engine_caller) on both engines:
+               host-visible ms per token and us per call, split into the
+               host quantize, the clean / invalidate copies and start + wait
   cpu_baseline the NumPy restatement of the contract on one core, and the
                C restatement on all cores, over one decode step
 All launches come from C through the library's ABI; Python only sets them up.
@@ -165,6 +170,22 @@ def time_gemm(torch, kv, cf, m, mrows, stream):
             "tops": round(2 * mrows * m.rows * m.k / us / 1e6, 2)}
 
 
+CALLER = os.path.join(ROOT, "llm-kv260_amd", "caller", "engine_caller")
+
+
+def run_caller(tokens=20):
+    """The reference's caller through the reference ABI, in a process of its own
+    (it opens its own device context and pools), on the gemv2 and v1 engines."""
+    import subprocess
+    out = {}
+    for name, extra in (("gemv2", []), ("v1", ["--v1"])):
+        p = subprocess.run([CALLER, "--tokens", str(tokens), *extra], capture_output=True, text=True, timeout=300)
+        if p.returncode != 0:
+            raise RuntimeError(f"engine_caller {name} failed: {p.stderr[-500:]}")
+        out[name] = json.loads(p.stdout.strip().splitlines()[-1])
+    return out
+
+
 def cpu_baseline(chain, mats, xs, budget_s=30.0):
     """One decode step through the NumPy restatement of q4_0.py (1 core), and the
     same step through the scalar C restatement with OpenMP over rows (all cores)."""
@@ -269,6 +290,10 @@ def main() -> int:
     lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 
     traffic = pmc_traffic() or {}
+    log("the reference's caller through the reference ABI (host-visible)")
+    caller = run_caller()
+    for name, r in caller.items():
+        log(f"caller {name}: {r['ms_per_token']:.3f} ms/token, {r['us_per_call']['total']:.1f} us/call host-visible")
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
@@ -315,6 +340,7 @@ def main() -> int:
                   "dependency": "none inside a step (w4a8_gemv_batch); steps in order"},
         "gemv": gemv,
         "gemm": gemm,
+        "caller": caller,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }
