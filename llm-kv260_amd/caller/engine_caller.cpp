@@ -29,7 +29,14 @@
 // (tp_llama's NEON quantize_x rounds with vcvta; the two agree except where
 // |s| + 0.5 rounds up in fp32.)
 //
-// Usage: engine_caller [--v1] [--tokens N] [--layers L] [--dump DIR]
+// With --gguf PATH the model comes from a GGUF file instead, as load_model
+// reads it (:226-287): hyperparameters from the llama.* keys, and every Q4_0
+// tensor's rows copied from the mapped file into the pools as they lie
+// (q|k|v and gate|up fused, token_embd as the LM head). The file is read
+// with the library's GGUF reader (include/w4a8_gguf.h), which stands where
+// the reference uses llama.cpp's gguf API.
+//
+// Usage: engine_caller [--v1] [--tokens N] [--layers L] [--gguf PATH] [--dump DIR]
 // Prints one JSON line with the per-call and per-token times. --dump DIR writes
 // the first token's inputs and outputs of layer 0's q|k|v, o and down, and of
 // the LM head, for an outside check.
@@ -47,6 +54,7 @@ extern "C" {
 #include "gemv2_dev.h"
 #include "gemv_dev.h"
 #include "udmabuf.h"
+#include "w4a8_gguf.h"
 }
 
 #define DIE(...)                                       \
@@ -299,12 +307,39 @@ struct engine_t {
 
 // ------------------------------------------------------------------ model
 
-// Llama-3.2-1B at one rank (board/tp/tp_llama.cpp:231-243 with nranks = 1).
-constexpr int N_EMBD = 2048, N_FF = 8192, N_HEAD = 32, N_HEAD_KV = 8, HEAD_DIM = 64, N_VOCAB = 128256;
-constexpr int Q_ROWS = N_EMBD, KV_ROWS = N_HEAD_KV * HEAD_DIM;
+// The model's shape at one rank (board/tp/tp_llama.cpp:231-243 with nranks = 1):
+// Llama-3.2-1B unless a GGUF file says otherwise.
+struct hparams {
+    int n_layer = 16, n_embd = 2048, n_ff = 8192, n_head = 32, n_head_kv = 8, n_vocab = 128256;
+    int head_dim() const { return n_embd / n_head; }
+    int kv_rows() const { return n_head_kv * head_dim(); }
+};
 
 struct layer_w {
     qmat qkv, o, gateup, down;
+};
+
+// A GGUF file as load_model reads it (gguf_file, tp_llama.cpp:149-188).
+struct gguf_file {
+    w4a8_gguf *g = nullptr;
+    void open(const char *path) {
+        if (w4a8_gguf_open(path, &g) != 0) DIE("cannot read %s", path);
+    }
+    void close() { w4a8_gguf_close(g); }
+    const uint8_t *data(const char *name, int rows, int k) const {
+        const int64_t i = w4a8_gguf_find_tensor(g, name);
+        if (i < 0) DIE("tensor %s missing", name);
+        w4a8_gguf_tensor t;
+        w4a8_gguf_tensor_info(g, i, &t);
+        if (t.type != W4A8_GGML_TYPE_Q4_0 || t.n_dims != 2 || t.ne[0] != (uint64_t)k || t.ne[1] != (uint64_t)rows)
+            DIE("tensor %s is not Q4_0 [%d, %d]", name, k, rows);
+        return (const uint8_t *)w4a8_gguf_tensor_data(g, i);
+    }
+    uint32_t u32(const char *key) const {
+        uint32_t v;
+        if (w4a8_gguf_get_u32(g, key, &v) != 0) DIE("key %s missing", key);
+        return v;
+    }
 };
 
 static void write_file(const std::string &path, const void *p, size_t n) {
@@ -325,47 +360,81 @@ static std::vector<uint8_t> plain_bytes(const qmat &m) {
 
 int main(int argc, char **argv) {
     bool want_v2 = true;
-    int tokens = 8, n_layer = 16;
-    std::string dump;
+    int tokens = 8, layers_arg = 0;
+    std::string dump, gguf;
     for (int i = 1; i < argc; ++i) {
         if (!strcmp(argv[i], "--v1")) want_v2 = false;
         else if (!strcmp(argv[i], "--tokens") && i + 1 < argc) tokens = atoi(argv[++i]);
-        else if (!strcmp(argv[i], "--layers") && i + 1 < argc) n_layer = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--layers") && i + 1 < argc) layers_arg = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--dump") && i + 1 < argc) dump = argv[++i];
-        else DIE("usage: engine_caller [--v1] [--tokens N] [--layers L] [--dump DIR]");
+        else if (!strcmp(argv[i], "--gguf") && i + 1 < argc) gguf = argv[++i];
+        else DIE("usage: engine_caller [--v1] [--tokens N] [--layers L] [--gguf PATH] [--dump DIR]");
     }
-    if (tokens < 1 || n_layer < 1 || n_layer > 16) DIE("need tokens >= 1 and 1 <= layers <= 16");
+    if (tokens < 1 || layers_arg < 0) DIE("need tokens >= 1 and layers >= 1");
 
     engine_t E;
     E.probe(want_v2);
     pools_t pools;
     pools.open();
     const double t_load0 = now();
-    std::vector<layer_w> layers(n_layer);
-    size_t total = 0;
+    hparams h;
+    gguf_file f;
+    if (!gguf.empty()) {
+        f.open(gguf.c_str());
+        h.n_layer = (int)f.u32("llama.block_count");
+        h.n_embd = (int)f.u32("llama.embedding_length");
+        h.n_ff = (int)f.u32("llama.feed_forward_length");
+        h.n_head = (int)f.u32("llama.attention.head_count");
+        h.n_head_kv = (int)f.u32("llama.attention.head_count_kv");
+        h.n_vocab = (int)f.u32("llama.vocab_size");
+    }
+    if (layers_arg > 0) h.n_layer = layers_arg < h.n_layer ? layers_arg : h.n_layer;
+    const int Q_ROWS = h.n_embd, KV_ROWS = h.kv_rows();
+    for (int v : {Q_ROWS + 2 * KV_ROWS, h.n_embd, 2 * h.n_ff, h.n_vocab})
+        if (v % 32) DIE("rows %d not a multiple of 32", v);
+    for (int v : {h.n_embd, h.n_ff})
+        if (v % 256 || v > 8192) DIE("width %d unusable by the engine", v);
+
+    // Row-major Q4_0 of one tensor: from the file, or synthetic and seeded.
+    std::vector<uint8_t> scratch;
     uint64_t seed = 1000;
-    for (int l = 0; l < n_layer; ++l) {
+    char name[96];
+    auto tensor = [&](int l, const char *what, int rows, int k) -> const uint8_t * {
+        if (l >= 0) snprintf(name, sizeof name, "blk.%d.%s.weight", l, what);
+        else snprintf(name, sizeof name, "%s.weight", what);
+        if (f.g) return f.data(name, rows, k);
+        scratch = synth_tensor(rows, k, seed++);
+        return scratch.data();
+    };
+    std::vector<layer_w> layers(h.n_layer);
+    size_t total = 0;
+    for (int l = 0; l < h.n_layer; ++l) {
         layer_w &L = layers[l];
-        L.qkv = new_mat(pools, Q_ROWS + 2 * KV_ROWS, N_EMBD, E.v2);
-        copy_rows(L.qkv, synth_tensor(Q_ROWS, N_EMBD, seed++).data(), N_EMBD, 0, Q_ROWS, 0);
-        copy_rows(L.qkv, synth_tensor(KV_ROWS, N_EMBD, seed++).data(), N_EMBD, 0, KV_ROWS, Q_ROWS);
-        copy_rows(L.qkv, synth_tensor(KV_ROWS, N_EMBD, seed++).data(), N_EMBD, 0, KV_ROWS, Q_ROWS + KV_ROWS);
-        L.o = new_mat(pools, N_EMBD, N_EMBD, E.v2);
-        copy_rows(L.o, synth_tensor(N_EMBD, N_EMBD, seed++).data(), N_EMBD, 0, N_EMBD, 0);
-        L.gateup = new_mat(pools, 2 * N_FF, N_EMBD, E.v2);
-        copy_rows(L.gateup, synth_tensor(N_FF, N_EMBD, seed++).data(), N_EMBD, 0, N_FF, 0);
-        copy_rows(L.gateup, synth_tensor(N_FF, N_EMBD, seed++).data(), N_EMBD, 0, N_FF, N_FF);
-        L.down = new_mat(pools, N_EMBD, N_FF, E.v2);
-        copy_rows(L.down, synth_tensor(N_EMBD, N_FF, seed++).data(), N_FF, 0, N_EMBD, 0);
+        L.qkv = new_mat(pools, Q_ROWS + 2 * KV_ROWS, h.n_embd, E.v2);
+        copy_rows(L.qkv, tensor(l, "attn_q", Q_ROWS, h.n_embd), h.n_embd, 0, Q_ROWS, 0);
+        copy_rows(L.qkv, tensor(l, "attn_k", KV_ROWS, h.n_embd), h.n_embd, 0, KV_ROWS, Q_ROWS);
+        copy_rows(L.qkv, tensor(l, "attn_v", KV_ROWS, h.n_embd), h.n_embd, 0, KV_ROWS, Q_ROWS + KV_ROWS);
+        L.o = new_mat(pools, h.n_embd, h.n_embd, E.v2);
+        copy_rows(L.o, tensor(l, "attn_output", h.n_embd, h.n_embd), h.n_embd, 0, h.n_embd, 0);
+        L.gateup = new_mat(pools, 2 * h.n_ff, h.n_embd, E.v2);
+        copy_rows(L.gateup, tensor(l, "ffn_gate", h.n_ff, h.n_embd), h.n_embd, 0, h.n_ff, 0);
+        copy_rows(L.gateup, tensor(l, "ffn_up", h.n_ff, h.n_embd), h.n_embd, 0, h.n_ff, h.n_ff);
+        L.down = new_mat(pools, h.n_embd, h.n_ff, E.v2);
+        copy_rows(L.down, tensor(l, "ffn_down", h.n_embd, h.n_ff), h.n_ff, 0, h.n_embd, 0);
         total += L.qkv.bytes() + L.o.bytes() + L.gateup.bytes() + L.down.bytes();
     }
-    qmat lm_head = new_mat(pools, N_VOCAB, N_EMBD, E.v2);
-    copy_rows(lm_head, synth_tensor(N_VOCAB, N_EMBD, seed++).data(), N_EMBD, 0, N_VOCAB, 0);
+    // The LM head is token_embd's rows (tp_llama.cpp:273-275).
+    qmat lm_head = new_mat(pools, h.n_vocab, h.n_embd, E.v2);
+    copy_rows(lm_head, tensor(-1, "token_embd", h.n_vocab, h.n_embd), h.n_embd, 0, h.n_vocab, 0);
     total += lm_head.bytes();
-    E.open(pools, N_VOCAB);
+    scratch.clear();
+    scratch.shrink_to_fit();
+    if (f.g) f.close();
+    E.open(pools, (size_t)h.n_vocab);
     // Everything the engine reads was written by the CPU: clean once.
     for (auto &p : pools.p) udmabuf_clean(p.base, p.used);
     const double t_load = now() - t_load0;
+    const int n_layer = h.n_layer, N_EMBD = h.n_embd, N_FF = h.n_ff, N_VOCAB = h.n_vocab;
 
     std::vector<float> x(N_FF);
     rng_t gx(7);

@@ -2,6 +2,7 @@
 #include <stdint.h>
 
 #include "../../include/w4a8.h"
+#include "../../include/w4a8_gguf.h"
 #include "kernels.h"
 
 using namespace w4a8;
@@ -54,6 +55,7 @@ const char *w4a8_strerror(int status) {
         case W4A8_ERR_ALIGN: return "pointer not aligned (weights and activations 16 B, output 4 B)";
         case W4A8_ERR_HIP: return "HIP runtime error";
         case W4A8_ERR_NODEV: return "no usable gfx950 device";
+        case W4A8_ERR_FORMAT: return "not a GGUF file, or a malformed one";
         default: return "unknown status";
     }
 }

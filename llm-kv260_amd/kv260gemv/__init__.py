@@ -38,6 +38,11 @@ EXPORTS = (
     "w4a8_gemv", "w4a8_gemv_q8_0", "w4a8_gemv_f32", "w4a8_gemv_quarters",
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
     "w4a8_chain_gemv", "w4a8_gemv_batch",
+    # w4a8_gguf.h
+    "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
+    "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
+    "w4a8_gguf_kv_type", "w4a8_gguf_get_u32", "w4a8_gguf_get_i32", "w4a8_gguf_get_u64", "w4a8_gguf_get_f32",
+    "w4a8_gguf_get_str", "w4a8_gguf_tensor_info", "w4a8_gguf_tensor_data", "w4a8_gguf_upload",
     # gemv_dev.h
     "gemv_dev_open", "gemv_dev_open_named", "gemv_dev_close", "gemv_dev_run",
     "gemv_dev_start", "gemv_dev_wait", "gemv_dev_start4",
