@@ -150,6 +150,30 @@ def time_gemv(torch, kv, cf, m, stream):
             "weight_copies": copies, "rotated_mb": round(copies * m.weight_bytes / 2**20, 1)}
 
 
+def time_lm_argmax(torch, kv, cf, stream):
+    """us per LM-head GEMV with the greedy argmax fused (w4a8_gemv_f32_argmax),
+    fp32 activation, three rotating weight copies as for the plain LM head."""
+    L = kv.lib()
+    m = cf.LM_HEAD
+    base = device_weights(torch, kv, m.rows, m.k, 7)
+    mats = [base] + [base.clone() for _ in range(2)]
+    x = torch.from_numpy(cf.activation(m)).cuda()
+    y = torch.empty(m.rows, dtype=torch.float32, device="cuda")
+    best = torch.empty(1, dtype=torch.int32, device="cuda")
+    ws = kv.argmax_workspace()
+    nbytes = ws.numel()
+    launches = 30
+    calls = [(lambda w: (lambda s: kv.check("w4a8_gemv_f32_argmax", L.w4a8_gemv_f32_argmax(
+        w.data_ptr(), x.data_ptr(), y.data_ptr(), m.rows, m.k, best.data_ptr(), ws.data_ptr(), nbytes, s))))(
+        mats[i % 3]) for i in range(launches)]
+    g = graph_of(torch, stream, calls)
+    ms, _ = time_replays(torch, stream, g, 10, 2)
+    us = ms * 1e3 / launches
+    del g, mats, base
+    return {"shape": f"{m.rows}x{m.k}", "us": round(us, 3), "gbps": round(m.algorithmic_bytes / us / 1e3, 1),
+            "argmax": int(best.cpu()[0]), "weight_copies": 3}
+
+
 def time_gemm(torch, kv, cf, m, mrows, stream):
     """us per M > 1 GEMM (engine-layout activation rows), rotating weight copies."""
     L = kv.lib()
@@ -286,6 +310,8 @@ def main() -> int:
                 gemm.append(dict(name=m.name, **r))
                 log(f"gemm {m.name} M={mrows}: {r['us']} us, {r['gbps']} GB/s, {r['tops']} TOP/s")
             torch.cuda.empty_cache()
+    lm_argmax = time_lm_argmax(torch, kv, cf, stream)
+    log(f"gemv lm_head + argmax: {lm_argmax['us']} us, {lm_argmax['gbps']} GB/s")
     lm = gemv["lm_head"]
     lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 
@@ -340,6 +366,7 @@ def main() -> int:
                   "dependency": "none inside a step (w4a8_gemv_batch); steps in order"},
         "gemv": gemv,
         "gemm": gemm,
+        "lm_head_argmax": lm_argmax,
         "caller": caller,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),

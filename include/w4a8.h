@@ -70,6 +70,19 @@ int w4a8_gemv_q8_0(const void *w, const void *x_blocks, float *y, int rows, int 
  * (gemv_q4_0_f32, src/llm_kv260/q4_0.py:185-188). */
 int w4a8_gemv_f32(const void *w, const float *x, float *y, int rows, int k, void *stream);
 
+/* The LM head with its greedy pick in one launch: y = W x as w4a8_gemv_f32,
+ * and *argmax (device int32) = the first row of the largest y, the reference's
+ * "if (y[i] > y[best]) best = i" scan (board/tp/tp_llama.cpp:879-880): ties go
+ * to the smaller row, -0 equals +0, a NaN is never picked, and a NaN at row 0
+ * gives 0 as the scan does. Each workgroup reduces its rows and the last one
+ * to finish reduces the workgroups' results, through `workspace`: device
+ * memory of w4a8_argmax_workspace_bytes() bytes, 16-byte aligned, zero-filled
+ * once before its first use (every call leaves it zero again). Calls that
+ * share a workspace must not run concurrently. */
+size_t w4a8_argmax_workspace_bytes(void);
+int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int k, int32_t *argmax,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
 /* Four row quarters at their own addresses, rows/4 contiguous rows each,
  * y contiguous (gemv_dev_start4, board/kv260gemv/gemv_dev.h:29-35). rows % 4 == 0. */
 int w4a8_gemv_quarters(const void *const w[4], const void *x, float *y, int rows, int k, void *stream);

@@ -81,6 +81,17 @@ int w4a8_gemv_f32(const void *w, const float *x, float *y, int rows, int k, void
     return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream));
 }
 
+size_t w4a8_argmax_workspace_bytes(void) { return argmax_workspace_bytes(); }
+
+int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int k, int32_t *argmax,
+                         void *workspace, size_t workspace_bytes, void *stream) {
+    if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    if (!argmax || !workspace) return W4A8_ERR_NULL;
+    if (!aligned(argmax, 4) || !aligned(workspace, 16)) return W4A8_ERR_ALIGN;
+    if (workspace_bytes < argmax_workspace_bytes()) return W4A8_ERR_SHAPE;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream, argmax, workspace));
+}
+
 int w4a8_gemv_quarters(const void *const w[4], const void *x, float *y, int rows, int k, void *stream) {
     if (!w) return W4A8_ERR_NULL;
     for (int q = 0; q < 4; ++q) {

@@ -72,7 +72,35 @@ struct GemvParams {
     int rpw;          // rows per wave tile, 64 / C
     int tiles;        // ceil(rows / rpw)
     int paired;       // v2 port layout
+    // Argmax epilogue (LM head): the first row of the largest y, written to
+    // *argmax by the last workgroup to finish; partials[workgroup] and the
+    // ticket counter live in the caller's workspace (the counter is zero
+    // between calls).
+    int32_t *argmax;
+    unsigned long long *partials;
+    unsigned int *ticket;
 };
+
+// Argmax key of y[row] = v: the largest v wins, and among equal values the
+// smallest row, which is the reference's scan (board/tp/tp_llama.cpp:879-880,
+// "if (y[i] > y[best]) best = i"). -0 compares equal to +0 there, so it is
+// keyed as +0; a NaN never compares greater, so it gets key 0 and never wins
+// (a NaN at row 0 is handled by the last workgroup: the scan starts there and
+// then keeps 0). Every other value has key > 0.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
+    if (v != v) return 0ull;
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row);
+}
+
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max_u64(v, __shfl_xor(v, off));
+    return v;
+}
 
 #ifndef W4A8_BATCH_WAVES
 #define W4A8_BATCH_WAVES 4
@@ -217,6 +245,8 @@ __device__ __forceinline__ void chunk_terms(const uint32_t w[CHUNK_DWORDS], cons
 }
 
 constexpr int TILE_BYTES = 64 * CHUNK_BYTES;   // 9,216
+// Argmax workspace: the ticket counter in its own 64-byte line, then the partials.
+constexpr size_t ARGMAX_PARTIALS_OFFSET = 64;
 // Tiles per wave held in registers: three for plain matrices; two for the
 // board layouts, whose per-lane address tables take the third's registers.
 template <bool PLAIN>
@@ -274,7 +304,46 @@ __device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t y, int byte_off, 
 
 // ONE_PASS: a tile holds at most eight rows (K >= 2048), so one pass of the
 // ordered sums covers it and each lane stores at most one value per tile.
-template <int XF, bool PLAIN, bool ONE_PASS>
+// The workgroup's best key (its waves' keys through LDS), published as this
+// workgroup's partial; the last workgroup to arrive reduces all partials,
+// writes the row, and sets the ticket back to zero for the next call.
+__device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long long best, int block, int nblocks,
+                                              uint8_t *lds) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    unsigned long long *keys = reinterpret_cast<unsigned long long *>(lds);   // the slabs are free by now
+    __shared__ int last;
+    best = wave_max_u64(best);
+    __syncthreads();
+    if (lane == 0) keys[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long b = 0;
+        for (int w = 0; w < waves; ++w) b = max_u64(b, keys[w]);
+        __hip_atomic_store(&P.partials[block], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned t = __hip_atomic_fetch_add(P.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = t == (unsigned)(nblocks - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    __atomic_thread_fence(__ATOMIC_ACQUIRE);
+    unsigned long long b = 0;
+    for (int i = tid; i < nblocks; i += blockDim.x)
+        b = max_u64(b, __hip_atomic_load(&P.partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    b = wave_max_u64(b);
+    __syncthreads();
+    if (lane == 0) keys[wave] = b;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long k = 0;
+        for (int w = 0; w < waves; ++w) k = max_u64(k, keys[w]);
+        const float y0 = __hip_atomic_load(&P.y[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t row = (k == 0ull || y0 != y0) ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)k);
+        __hip_atomic_store(P.argmax, row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(P.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false>
 __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
@@ -345,6 +414,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     };
 
     const int acc_r = lane >> 3, acc_a = lane & 7;
+    unsigned long long best = 0;          // argmax epilogue: this lane's best key
     const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * P.rows, BUFFER_DWORD3);
     // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
     // slab -> ordered lane sums -> tree -> y; with REFILL the buffer then
@@ -398,12 +468,19 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
             const int row = tile * rpw + acc_r;
-            store_y(y_rsrc, acc_r < rpw && acc_a == 0 && row < P.rows ? 4 * row : OUT_OF_RANGE, yv);
+            const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
+            store_y(y_rsrc, mine ? 4 * row : OUT_OF_RANGE, yv);
+            if constexpr (ARGMAX) {
+                if (mine) best = max_u64(best, argmax_key(yv, row));
+            }
         } else {
             for (int r = acc_r; r - acc_r < rpw; r += 8) {
                 const float yv = tree8_dpp(lane_sum(r));
                 const int row = tile * rpw + r;
-                if (r < rpw && acc_a == 0 && row < P.rows) P.y[row] = yv;
+                if (r < rpw && acc_a == 0 && row < P.rows) {
+                    P.y[row] = yv;
+                    if constexpr (ARGMAX) best = max_u64(best, argmax_key(yv, row));
+                }
             }
         }
         wave_sync_lds();
@@ -438,12 +515,13 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     } else {
         stage_x();
     }
+    if constexpr (ARGMAX) argmax_finish(P, best, block, nblocks, lds);
 }
 
-template <int XF, bool PLAIN, bool ONE_PASS>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false>
 __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    gemv_m1_body<XF, PLAIN, ONE_PASS>(P, blockIdx.x, gridDim.x, lds);
+    gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX>(P, blockIdx.x, gridDim.x, lds);
 }
 
 __host__ __device__ inline void derive_plain(GemvParams &P, const uint8_t *w, const void *x, float *y, int rows, int k) {
@@ -489,29 +567,35 @@ __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2
     gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, lds);
 }
 
-template <int XF, bool PLAIN, bool ONE_PASS>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX>
 hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
     // Dynamic LDS above the default 64 KB must be allowed per kernel once.
     static bool lds_allowed = false;
+    const void *fn = reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX>);
     if (!lds_allowed) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BUDGET);
+        // What the kernel's static LDS (the argmax flag) leaves of the budget.
+        hipFuncAttributes attr{};
+        hipError_t e = hipFuncGetAttributes(&attr, fn);
+        if (e != hipSuccess) return e;
+        e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(LDS_BUDGET - attr.sharedSizeBytes));
         if (e != hipSuccess) return e;
         lds_allowed = true;
     }
-    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS>), dim3(grid), dim3(threads), lds, stream, P);
+    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX>), dim3(grid), dim3(threads), lds, stream, P);
     return hipGetLastError();
 }
 
-template <int XF, bool PLAIN>
+template <int XF, bool PLAIN, bool ARGMAX>
 hipError_t launch_xf(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
-    return P.rpw <= 8 ? launch_pass<XF, PLAIN, true>(P, grid, threads, lds, stream)
-                      : launch_pass<XF, PLAIN, false>(P, grid, threads, lds, stream);
+    return P.rpw <= 8 ? launch_pass<XF, PLAIN, true, ARGMAX>(P, grid, threads, lds, stream)
+                      : launch_pass<XF, PLAIN, false, ARGMAX>(P, grid, threads, lds, stream);
 }
 
-template <int XF>
+template <int XF, bool ARGMAX = false>
 hipError_t launch_layout(const GemvParams &P, bool plain, int grid, int threads, size_t lds, hipStream_t stream) {
-    return plain ? launch_xf<XF, true>(P, grid, threads, lds, stream) : launch_xf<XF, false>(P, grid, threads, lds, stream);
+    return plain ? launch_xf<XF, true, ARGMAX>(P, grid, threads, lds, stream)
+                 : launch_xf<XF, false, ARGMAX>(P, grid, threads, lds, stream);
 }
 
 }  // namespace
@@ -528,8 +612,16 @@ int device_cu_count() {
     return cached[dev];
 }
 
-hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream) {
+size_t argmax_workspace_bytes() { return ARGMAX_PARTIALS_OFFSET + 8 * (size_t)(2 * device_cu_count()); }
+
+hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream,
+                          int32_t *argmax, void *workspace) {
     GemvParams P{};
+    if (argmax) {
+        P.argmax = argmax;
+        P.ticket = static_cast<unsigned int *>(workspace);
+        P.partials = reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(workspace) + ARGMAX_PARTIALS_OFFSET);
+    }
     for (int s = 0; s < 4; ++s) P.seg[s] = s < w.nseg ? w.seg[s] : w.seg[0];
     P.x = x;
     P.y = y;
@@ -569,6 +661,12 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     }
     const int threads = 64 * waves;
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
+    if (argmax) {
+        // The workspace holds one partial per workgroup: at most two per CU.
+        if (grid > 2 * cus) return hipErrorInvalidValue;
+        if (xf != X_F32) return hipErrorInvalidValue;
+        return launch_layout<X_F32, true>(P, plain, grid, threads, lds, stream);
+    }
     switch (xf) {
         case X_ENGINE: return launch_layout<X_ENGINE>(P, plain, grid, threads, lds, stream);
         case X_Q8_0: return launch_layout<X_Q8_0>(P, plain, grid, threads, lds, stream);

@@ -36,7 +36,12 @@ constexpr int MAX_K_GEMM = 16384;
 
 int device_cu_count();            // of the current device (cached per device)
 
-hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream);
+// argmax != null: also *argmax = the first row of the largest y, reduced in the
+// same launch through `workspace` (argmax_workspace_bytes(), zero between
+// calls); x must then be X_F32.
+hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream,
+                          int32_t *argmax = nullptr, void *workspace = nullptr);
+size_t argmax_workspace_bytes();   // of the current device
 
 // y[m][rows] for m activation rows in engine layout (row stride K + K/8 bytes).
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, float *y, hipStream_t stream);

@@ -37,7 +37,7 @@ EXPORTS = (
     "w4a8_q4_0_row_bytes", "w4a8_engine_x_bytes", "w4a8_q8_0_row_bytes",
     "w4a8_gemv", "w4a8_gemv_q8_0", "w4a8_gemv_f32", "w4a8_gemv_quarters",
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
-    "w4a8_chain_gemv", "w4a8_gemv_batch",
+    "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -97,6 +97,10 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).restype = i
     L.w4a8_gemm.argtypes = [p, p, p, i, i, i, p]
     L.w4a8_gemm.restype = i
+    L.w4a8_argmax_workspace_bytes.argtypes = []
+    L.w4a8_argmax_workspace_bytes.restype = ctypes.c_size_t
+    L.w4a8_gemv_f32_argmax.argtypes = [p, p, p, i, i, p, p, ctypes.c_size_t, p]
+    L.w4a8_gemv_f32_argmax.restype = i
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
         getattr(L, f).argtypes = [p, i, p]
         getattr(L, f).restype = i
@@ -262,6 +266,30 @@ def gemv_q4_0_f32(blocks, k: int, x, out=None):
     check("w4a8_gemv_f32", lib().w4a8_gemv_f32(blocks.data_ptr(), x.data_ptr(), y.data_ptr(), n, k,
                                                _stream(blocks)))
     return y
+
+
+def argmax_workspace():
+    """A zero-filled workspace for gemv_q4_0_f32_argmax on the current device."""
+    import torch
+    return torch.zeros(lib().w4a8_argmax_workspace_bytes(), dtype=torch.uint8, device="cuda")
+
+
+def gemv_q4_0_f32_argmax(blocks, k: int, x, workspace, out=None):
+    """The LM head and its greedy pick in one launch: (y, argmax) with argmax an
+    int32 [1] GPU tensor holding the first row of the largest y
+    (board/tp/tp_llama.cpp:879-880). `workspace` comes from argmax_workspace()."""
+    import torch
+    _need(x, torch.float32, "x")
+    _check_blocks(blocks, k)
+    if tuple(x.shape) != (k,):
+        raise ValueError(f"x must be [{k}], got {tuple(x.shape)}")
+    n = blocks.shape[0]
+    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    best = torch.empty(1, dtype=torch.int32, device=blocks.device)
+    check("w4a8_gemv_f32_argmax", lib().w4a8_gemv_f32_argmax(
+        blocks.data_ptr(), x.data_ptr(), y.data_ptr(), n, k, best.data_ptr(), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(blocks)))
+    return y, best
 
 
 def gemv_q8_0_blocks(blocks, k: int, x_blocks, out=None):
