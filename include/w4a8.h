@@ -83,6 +83,28 @@ size_t w4a8_argmax_workspace_bytes(void);
 int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int k, int32_t *argmax,
                          void *workspace, size_t workspace_bytes, void *stream);
 
+/* The reference's producers of the GEMV input, fused into the GEMV's own
+ * activation staging (board/tp/tp_llama.cpp, computed as it does):
+ *   rmsnorm (:557-569): h = x * (1 / sqrtf((float)(ss / k) + eps)) * norm_w,
+ *     ss the float64 sum of x_i^2 in four lanes (i % 4, increasing i), met as
+ *     (l0 + l2) + (l1 + l3); the input of q|k|v, gate|up and the LM head
+ *     (:828-830, :854-856, :878-879). y = W Q8_0(h).
+ *   silu_mul (:612-619): a = silu(gate) * up with gate_up = gate | up,
+ *     float32[2k] (the gate|up GEMV's output), silu(g) = g / (1 + expf(-g))
+ *     through ggml's vector expf; the input of down (:858-860). y = W Q8_0(a).
+ * Each is byte-identical to the standalone producer below followed by
+ * w4a8_gemv. x, norm_w and gate_up 16-byte aligned. */
+int w4a8_gemv_rmsnorm(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
+                      void *stream);
+int w4a8_gemv_rmsnorm_argmax(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
+                             int32_t *argmax, void *workspace, size_t workspace_bytes, void *stream);
+int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, int k, void *stream);
+
+/* The same producers on their own, m rows, quantized to the engine layout
+ * (row stride w4a8_engine_x_bytes(k)): the input of w4a8_gemv / w4a8_gemm. */
+int w4a8_rmsnorm_q8_0(const float *x, const float *norm_w, float eps, void *out_engine, int k, int m, void *stream);
+int w4a8_silu_mul_q8_0(const float *gate_up, void *out_engine, int k, int m, void *stream);
+
 /* Four row quarters at their own addresses, rows/4 contiguous rows each,
  * y contiguous (gemv_dev_start4, board/kv260gemv/gemv_dev.h:29-35). rows % 4 == 0. */
 int w4a8_gemv_quarters(const void *const w[4], const void *x, float *y, int rows, int k, void *stream);

@@ -92,6 +92,48 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
     return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream, argmax, workspace));
 }
 
+int w4a8_gemv_rmsnorm(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
+                      void *stream) {
+    if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    if (!norm_w) return W4A8_ERR_NULL;
+    if (!aligned(norm_w, 16)) return W4A8_ERR_ALIGN;
+    XAux aux;
+    aux.norm_w = norm_w;
+    aux.eps = eps;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_RMS, y, (hipStream_t)stream, nullptr, nullptr, aux));
+}
+
+int w4a8_gemv_rmsnorm_argmax(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
+                             int32_t *argmax, void *workspace, size_t workspace_bytes, void *stream) {
+    if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    if (!norm_w || !argmax || !workspace) return W4A8_ERR_NULL;
+    if (!aligned(norm_w, 16) || !aligned(argmax, 4) || !aligned(workspace, 16)) return W4A8_ERR_ALIGN;
+    if (workspace_bytes < argmax_workspace_bytes()) return W4A8_ERR_SHAPE;
+    XAux aux;
+    aux.norm_w = norm_w;
+    aux.eps = eps;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_RMS, y, (hipStream_t)stream, argmax, workspace, aux));
+}
+
+int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, int k, void *stream) {
+    if (int s = check_gemv(w, gate_up, y, rows, k, 16)) return s;
+    return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), gate_up, X_SILU, y, (hipStream_t)stream));
+}
+
+int w4a8_rmsnorm_q8_0(const float *x, const float *norm_w, float eps, void *out_engine, int k, int m, void *stream) {
+    if (!x || !norm_w || !out_engine) return W4A8_ERR_NULL;
+    if (check_k(k) || m < 1) return W4A8_ERR_SHAPE;
+    if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(out_engine, 16)) return W4A8_ERR_ALIGN;
+    return hip_status(launch_rmsnorm_q8_0(x, norm_w, eps, k, m, static_cast<uint8_t *>(out_engine), (hipStream_t)stream));
+}
+
+int w4a8_silu_mul_q8_0(const float *gate_up, void *out_engine, int k, int m, void *stream) {
+    if (!gate_up || !out_engine) return W4A8_ERR_NULL;
+    if (check_k(k) || m < 1) return W4A8_ERR_SHAPE;
+    if (!aligned(gate_up, 16) || !aligned(out_engine, 16)) return W4A8_ERR_ALIGN;
+    return hip_status(launch_silu_mul_q8_0(gate_up, k, m, static_cast<uint8_t *>(out_engine), (hipStream_t)stream));
+}
+
 int w4a8_gemv_quarters(const void *const w[4], const void *x, float *y, int rows, int k, void *stream) {
     if (!w) return W4A8_ERR_NULL;
     for (int q = 0; q < 4; ++q) {

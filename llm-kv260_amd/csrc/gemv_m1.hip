@@ -79,6 +79,9 @@ struct GemvParams {
     int32_t *argmax;
     unsigned long long *partials;
     unsigned int *ticket;
+    // X_RMS: the norm weight float32[k] and epsilon.
+    const float *norm_w;
+    float eps;
 };
 
 // Argmax key of y[row] = v: the largest v wins, and among equal values the
@@ -160,11 +163,37 @@ template <>
 struct XRaw<X_F32> {
     float4 v[8];
 };
+template <>
+struct XRaw<X_RMS> {
+    float4 v[8];   // x
+    float4 w[8];   // norm weight
+};
+template <>
+struct XRaw<X_SILU> {
+    float4 g[8];   // gate
+    float4 u[8];   // up
+};
+
+__device__ __forceinline__ void load_f32_block(__amdgpu_buffer_rsrc_t rb, int off, float4 v[8]) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rb, off == OUT_OF_RANGE ? OUT_OF_RANGE : off + 16 * m, 0, 0);
+        v[m] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
+    }
+}
 
 // Block b of the activation; a lane with live == false reads nothing.
 template <int XF>
-__device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, XRaw<XF> &r) {
-    if constexpr (XF == X_ENGINE) {
+__device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, XRaw<XF> &r,
+                                       const float *norm_w = nullptr) {
+    if constexpr (XF == X_RMS) {
+        load_f32_block(buffer_of(x, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.v);
+        load_f32_block(buffer_of(norm_w, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.w);
+    } else if constexpr (XF == X_SILU) {
+        const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(8 * k));
+        load_f32_block(xb, live ? 128 * b : OUT_OF_RANGE, r.g);
+        load_f32_block(xb, live ? 4 * k + 128 * b : OUT_OF_RANGE, r.u);
+    } else if constexpr (XF == X_ENGINE) {
         const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(k + k / 8));
         const int q_off = live ? 32 * b : OUT_OF_RANGE, d_off = live ? k + 4 * b : OUT_OF_RANGE;
         r.q0 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off, 0, 0);
@@ -188,7 +217,8 @@ __device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, X
 
 // Quantize (if fp32) and store block b into LDS: int8 values, fp32 scale, int8 sum.
 template <int XF>
-__device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_q, float *s_d, int32_t *s_s) {
+__device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_q, float *s_d, int32_t *s_s,
+                                        float rms_scale = 0.0f) {
     uint32_t q[8];
     float dx;
     if constexpr (XF == X_ENGINE) {
@@ -201,9 +231,31 @@ __device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_q,
         for (int m = 0; m < 8; ++m) q[m] = (uint32_t)r.h[1 + 2 * m] | ((uint32_t)r.h[2 + 2 * m] << 16);
     } else {
         float v[32];
+        if constexpr (XF == X_F32) {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            v[4 * m] = r.v[m].x; v[4 * m + 1] = r.v[m].y; v[4 * m + 2] = r.v[m].z; v[4 * m + 3] = r.v[m].w;
+            for (int m = 0; m < 8; ++m) {
+                v[4 * m] = r.v[m].x; v[4 * m + 1] = r.v[m].y; v[4 * m + 2] = r.v[m].z; v[4 * m + 3] = r.v[m].w;
+            }
+        } else if constexpr (XF == X_RMS) {
+            // out = (x * scale) * w, rmsnorm's last step (tp_llama.cpp:568).
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const float xv[4] = {r.v[m].x, r.v[m].y, r.v[m].z, r.v[m].w};
+                const float wv[4] = {r.w[m].x, r.w[m].y, r.w[m].z, r.w[m].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a = xv[e] * rms_scale;
+                    v[4 * m + e] = a * wv[e];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const float gv[4] = {r.g[m].x, r.g[m].y, r.g[m].z, r.g[m].w};
+                const float uv[4] = {r.u[m].x, r.u[m].y, r.u[m].z, r.u[m].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * m + e] = silu_mul(gv[e], uv[e]);
+            }
         }
         float amax = 0.0f;
 #pragma unroll
@@ -387,18 +439,42 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     // 1. The activation. Its loads go out before any weight tile's; the
     // staging below waits for them only.
     XRaw<XF> xr;
-    x_load<XF>(P.x, P.k, tid, tid < nb, xr);
+    x_load<XF>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
 
     uint32_t xv[8][8];
     float xd[8];
     int32_t xs[8];
     // 2. Stage the activation, then pull this lane's chunk column into registers.
     auto stage_x = [&]() {
-        if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s);
+        float rms = 0.0f;
+        if constexpr (XF == X_RMS) {
+            // rmsnorm's scale needs the whole of x: staged as fp32 after the
+            // block sums, reduced by wave 0, handed out through LDS.
+            float *xs = reinterpret_cast<float *>(s_s + nb);
+            float *s_rms = xs + P.k;
+            if (tid < nb) {
+#pragma unroll
+                for (int m = 0; m < 8; ++m) reinterpret_cast<float4 *>(xs + 32 * tid)[m] = xr.v[m];
+            }
+            for (int b = tid + nthreads; b < nb; b += nthreads) {
+                XRaw<XF> xb;
+                x_load<XF>(P.x, P.k, b, true, xb, P.norm_w);
+#pragma unroll
+                for (int m = 0; m < 8; ++m) reinterpret_cast<float4 *>(xs + 32 * b)[m] = xb.v[m];
+            }
+            __syncthreads();
+            if (wave == 0) {
+                const float sc = rms_scale_wave(xs, P.k, P.eps);
+                if (lane == 0) *s_rms = sc;
+            }
+            __syncthreads();
+            rms = *s_rms;
+        }
+        if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s, rms);
         for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
             XRaw<XF> xb;
-            x_load<XF>(P.x, P.k, b, true, xb);
-            x_stage<XF>(xb, b, s_q, s_d, s_s);
+            x_load<XF>(P.x, P.k, b, true, xb, P.norm_w);
+            x_stage<XF>(xb, b, s_q, s_d, s_s, rms);
         }
         __syncthreads();
         const int cb = lane_live ? 8 * my_c : 0;
@@ -615,8 +691,10 @@ int device_cu_count() {
 size_t argmax_workspace_bytes() { return ARGMAX_PARTIALS_OFFSET + 8 * (size_t)(2 * device_cu_count()); }
 
 hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream,
-                          int32_t *argmax, void *workspace) {
+                          int32_t *argmax, void *workspace, XAux aux) {
     GemvParams P{};
+    P.norm_w = aux.norm_w;
+    P.eps = aux.eps;
     if (argmax) {
         P.argmax = argmax;
         P.ticket = static_cast<unsigned int *>(workspace);
@@ -638,7 +716,9 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     const bool plain = w.nseg == 1 && !w.paired;
     const int cus = device_cu_count();
     const int nb = w.k / QK;
-    const size_t x_lds = (size_t)nb * 40;
+    // Staged activation: int8 values, fp32 scale and int32 sum per block; for
+    // X_RMS also x itself as fp32 and the rmsnorm scale.
+    const size_t x_lds = (size_t)nb * 40 + (xf == X_RMS ? (size_t)w.k * 4 + 16 : 0);
     // Small matrices: one tile per wave, workgroups spread over every CU
     // (each stages its own copy of x in parallel). Larger ones: at most eight
     // waves per CU (the register budget of three tiles per wave allows two
@@ -664,13 +744,16 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     if (argmax) {
         // The workspace holds one partial per workgroup: at most two per CU.
         if (grid > 2 * cus) return hipErrorInvalidValue;
-        if (xf != X_F32) return hipErrorInvalidValue;
-        return launch_layout<X_F32, true>(P, plain, grid, threads, lds, stream);
+        if (xf == X_F32) return launch_layout<X_F32, true>(P, plain, grid, threads, lds, stream);
+        if (xf == X_RMS) return launch_layout<X_RMS, true>(P, plain, grid, threads, lds, stream);
+        return hipErrorInvalidValue;
     }
     switch (xf) {
         case X_ENGINE: return launch_layout<X_ENGINE>(P, plain, grid, threads, lds, stream);
         case X_Q8_0: return launch_layout<X_Q8_0>(P, plain, grid, threads, lds, stream);
         case X_F32: return launch_layout<X_F32>(P, plain, grid, threads, lds, stream);
+        case X_RMS: return launch_layout<X_RMS>(P, plain, grid, threads, lds, stream);
+        case X_SILU: return launch_layout<X_SILU>(P, plain, grid, threads, lds, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -13,6 +13,14 @@ enum XFormat : int {
     X_ENGINE = 0,   // int8[K] then float32[K/32]  (pack_x_for_engine, q4_0.py:193-200)
     X_Q8_0 = 1,     // ggml Q8_0 blocks: fp16 d then 32 int8, 34 bytes each
     X_F32 = 2,      // float32[K], quantized to Q8_0 inside the kernel (fused)
+    X_RMS = 3,      // float32[K] x and float32[K] norm weight: rmsnorm, then Q8_0, inside the kernel
+    X_SILU = 4,     // float32[2K] gate | up: silu(gate) * up, then Q8_0, inside the kernel
+};
+
+// Extra inputs of the fused producer formats.
+struct XAux {
+    const float *norm_w = nullptr;   // X_RMS
+    float eps = 0.0f;
 };
 
 // Up to four row segments of one matrix: rows [s*seg_rows, (s+1)*seg_rows) live
@@ -38,9 +46,9 @@ int device_cu_count();            // of the current device (cached per device)
 
 // argmax != null: also *argmax = the first row of the largest y, reduced in the
 // same launch through `workspace` (argmax_workspace_bytes(), zero between
-// calls); x must then be X_F32.
+// calls); x must then be X_F32 or X_RMS.
 hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream,
-                          int32_t *argmax = nullptr, void *workspace = nullptr);
+                          int32_t *argmax = nullptr, void *workspace = nullptr, XAux aux = XAux{});
 size_t argmax_workspace_bytes();   // of the current device
 
 // y[m][rows] for m activation rows in engine layout (row stride K + K/8 bytes).
@@ -48,6 +56,12 @@ hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, 
 
 // x: float32[m][K] -> engine layout rows, or ggml Q8_0 block rows.
 hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFormat out_fmt, hipStream_t stream);
+// Producers of the activation, then Q8_0, to engine layout rows (K <= 16384):
+// rmsnorm (m rows of float32[K], norm weight float32[K]); silu(gate) * up
+// (m rows of float32[2K] gate | up).
+hipError_t launch_rmsnorm_q8_0(const float *x, const float *w, float eps, int k, int m, uint8_t *out,
+                               hipStream_t stream);
+hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out, hipStream_t stream);
 
 }  // namespace w4a8
 

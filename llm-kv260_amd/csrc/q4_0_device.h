@@ -117,3 +117,63 @@ __device__ __forceinline__ float tree8_dpp(float lane_sum) {
 }
 
 }  // namespace w4a8
+
+// ----------------------------------------------------------------------------
+// Producers of the activation, from the reference's decode loop
+// (board/tp/tp_llama.cpp): computed exactly as it does, so that the fused
+// kernels see the same float32 activation its CPU code would hand the engine.
+// Every operation is an IEEE one (fp64 adds, correctly rounded fp32 divide and
+// square root, fused multiply-adds where the reference fuses), with
+// -ffp-contract=off keeping everything else unfused.
+namespace w4a8 {
+
+// ggml's vector float32 exp (tp_llama.cpp:530-553, itself Arm's optimized-
+// routines expf, MIT): n = round(x / ln 2) by the 1.5 * 2^23 shift, the
+// remainder b = x - n ln 2 in two fused steps, a degree-5 polynomial in b
+// evaluated with fused multiply-adds, and 2^n built in the exponent bits, with
+// the two scalings that keep |n| > 126 and |n| > 192 in range. Same constants,
+// same operation order, same fused steps, one element at a time.
+__device__ __forceinline__ float ggml_vec_expf(float x) {
+    const float shift = 0x1.8p23f;
+    const float z = fmaf(x, 0x1.715476p+0f, shift);
+    const float n = z - shift;
+    const float b = fmaf(-n, 0x1.7f7d1cp-20f, fmaf(-n, 0x1.62e4p-1f, x));
+    const uint32_t e = __float_as_uint(z) << 23;
+    const float k = __uint_as_float(e + 0x3f800000u);
+    const float u = b * b;
+    const float j = fmaf(fmaf(fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u, fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)), u,
+                         0x1.ffffecp-1f * b);
+    if (!(fabsf(n) > 126.0f)) return fmaf(k, j, k);
+    const uint32_t d = n <= 0.0f ? 0x82000000u : 0u;
+    const float s1 = __uint_as_float(d + 0x7f000000u), s2 = __uint_as_float(e - d);
+    if (fabsf(n) > 192.0f) return s1 * s1;
+    return fmaf(s2, j, s2) * s1;
+}
+
+// silu(g) * u (silu_mul, tp_llama.cpp:612-619): g / (1 + exp(-g)), then * u.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float sg = g / (1.0f + ggml_vec_expf(-g));
+    return sg * u;
+}
+
+// rmsnorm's scale (tp_llama.cpp:557-569) over x[0..n) in LDS, n % 4 == 0: the
+// sum of squares accumulates in float64 in four lanes, element i in lane i % 4
+// in increasing i; the lanes meet as (l0 + l2) + (l1 + l3); then
+// 1 / sqrtf((float)(ss / n) + eps). Lanes 0..3 of the calling wave do the
+// four chains; the result is returned in every lane of the wave.
+__device__ __forceinline__ float rms_scale_wave(const float *xs, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    double acc = 0.0;
+    if (lane < 4) {
+#pragma unroll 8
+        for (int i = lane; i < n; i += 4) {
+            const double v = (double)xs[i];
+            acc = acc + v * v;
+        }
+    }
+    const double l1 = __shfl(acc, 1), l2 = __shfl(acc, 2), l3 = __shfl(acc, 3), l0 = __shfl(acc, 0);
+    const double ss = (l0 + l2) + (l1 + l3);
+    return 1.0f / sqrtf((float)(ss / (double)n) + eps);
+}
+
+}  // namespace w4a8

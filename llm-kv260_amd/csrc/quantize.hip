@@ -22,15 +22,11 @@ __device__ __forceinline__ void load_block(const float *src, float v[32]) {
     }
 }
 
+// Q8_0 of one 32-element block (q4_0.py:83-97), stored as block b of row `row`
+// of the engine layout (int8[k] | float32[k/32]) or of ggml Q8_0 blocks.
 template <int OUT>
-__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int k, int m,
-                                                            uint8_t *__restrict__ out) {
+__device__ __forceinline__ void quantize_store(const float v[32], int row, int b, int k, uint8_t *__restrict__ out) {
     const int nb = k >> 5;
-    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (long)nb * m) return;
-    const int row = (int)(gid / nb), b = (int)(gid - (long)row * nb);
-    float v[32];
-    load_block(x + (size_t)row * k + 32 * b, v);
     float amax = 0.0f;
 #pragma unroll
     for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
@@ -59,6 +55,64 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
             dst[1 + 2 * w] = (uint16_t)(q[w] & 0xFFFFu);
             dst[2 + 2 * w] = (uint16_t)(q[w] >> 16);
         }
+    }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int k, int m,
+                                                            uint8_t *__restrict__ out) {
+    const int nb = k >> 5;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long)nb * m) return;
+    const int row = (int)(gid / nb), b = (int)(gid - (long)row * nb);
+    float v[32];
+    load_block(x + (size_t)row * k + 32 * b, v);
+    quantize_store<OUT>(v, row, b, k, out);
+}
+
+// act = silu(gate) * up (tp_llama.cpp:612-619) of m rows gate | up
+// (float32[2k] each, the gate|up GEMV's output), quantized to the engine layout.
+__global__ __launch_bounds__(256) void silu_mul_q8_0_kernel(const float *__restrict__ gate_up, int k, int m,
+                                                            uint8_t *__restrict__ out) {
+    const int nb = k >> 5;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long)nb * m) return;
+    const int row = (int)(gid / nb), b = (int)(gid - (long)row * nb);
+    float g[32], u[32], v[32];
+    load_block(gate_up + (size_t)row * 2 * k + 32 * b, g);
+    load_block(gate_up + (size_t)row * 2 * k + k + 32 * b, u);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) v[e] = silu_mul(g[e], u[e]);
+    quantize_store<X_ENGINE>(v, row, b, k, out);
+}
+
+// h = rmsnorm(x) * norm_w (tp_llama.cpp:557-569) of m rows of float32[k],
+// quantized to the engine layout: one workgroup per row (the sum of squares
+// runs over the whole row), x staged in LDS for wave 0's four fp64 chains.
+__global__ __launch_bounds__(256) void rmsnorm_q8_0_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                           float eps, int k, uint8_t *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];
+    __shared__ float scale;
+    const int row = blockIdx.x, nb = k >> 5;
+    const float *xr = x + (size_t)row * k;
+    for (int i = threadIdx.x; i < k / 4; i += blockDim.x)
+        reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(xr)[i];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const float sc = rms_scale_wave(xs, k, eps);
+        if (threadIdx.x == 0) scale = sc;
+    }
+    __syncthreads();
+    const float sc = scale;
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        float wv[32], v[32];
+        load_block(w + 32 * b, wv);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float a = xs[32 * b + e] * sc;
+            v[e] = a * wv[e];
+        }
+        quantize_store<X_ENGINE>(v, row, b, k, out);
     }
 }
 
@@ -108,6 +162,30 @@ hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFor
         hipLaunchKernelGGL(quantize_q8_0_kernel<X_Q8_0>, dim3(grid), dim3(256), 0, stream, x, k, m, out);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out, hipStream_t stream) {
+    const long blocks = (long)(k / 32) * m;
+    if (blocks == 0) return hipSuccess;
+    const long grid = (blocks + 255) / 256;
+    if (grid > 0x7fffffffL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(silu_mul_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, stream, gate_up, k, m, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_q8_0(const float *x, const float *w, float eps, int k, int m, uint8_t *out,
+                               hipStream_t stream) {
+    if (m <= 0) return hipSuccess;
+    const size_t lds = (size_t)k * 4;
+    static bool lds_allowed = false;
+    if (!lds_allowed) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&rmsnorm_q8_0_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e != hipSuccess) return e;
+        lds_allowed = true;
+    }
+    hipLaunchKernelGGL(rmsnorm_q8_0_kernel, dim3((unsigned)m), dim3(256), lds, stream, x, w, eps, k, out);
     return hipGetLastError();
 }
 

@@ -38,6 +38,8 @@ EXPORTS = (
     "w4a8_gemv", "w4a8_gemv_q8_0", "w4a8_gemv_f32", "w4a8_gemv_quarters",
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
     "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
+    "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
+    "w4a8_silu_mul_q8_0",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -101,6 +103,17 @@ def lib() -> ctypes.CDLL:
     L.w4a8_argmax_workspace_bytes.restype = ctypes.c_size_t
     L.w4a8_gemv_f32_argmax.argtypes = [p, p, p, i, i, p, p, ctypes.c_size_t, p]
     L.w4a8_gemv_f32_argmax.restype = i
+    f32 = ctypes.c_float
+    L.w4a8_gemv_rmsnorm.argtypes = [p, p, p, f32, p, i, i, p]
+    L.w4a8_gemv_rmsnorm.restype = i
+    L.w4a8_gemv_rmsnorm_argmax.argtypes = [p, p, p, f32, p, i, i, p, p, ctypes.c_size_t, p]
+    L.w4a8_gemv_rmsnorm_argmax.restype = i
+    L.w4a8_gemv_silu_mul.argtypes = [p, p, p, i, i, p]
+    L.w4a8_gemv_silu_mul.restype = i
+    L.w4a8_rmsnorm_q8_0.argtypes = [p, p, f32, p, i, i, p]
+    L.w4a8_rmsnorm_q8_0.restype = i
+    L.w4a8_silu_mul_q8_0.argtypes = [p, p, i, i, p]
+    L.w4a8_silu_mul_q8_0.restype = i
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
         getattr(L, f).argtypes = [p, i, p]
         getattr(L, f).restype = i
@@ -290,6 +303,74 @@ def gemv_q4_0_f32_argmax(blocks, k: int, x, workspace, out=None):
         blocks.data_ptr(), x.data_ptr(), y.data_ptr(), n, k, best.data_ptr(), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream(blocks)))
     return y, best
+
+
+def gemv_rmsnorm(blocks, k: int, x, norm_w, eps: float, out=None):
+    """y = W Q8_0(rmsnorm(x) * norm_w), rmsnorm as board/tp/tp_llama.cpp:557-569, in one kernel."""
+    import torch
+    _need(x, torch.float32, "x")
+    _need(norm_w, torch.float32, "norm_w")
+    _check_blocks(blocks, k)
+    if tuple(x.shape) != (k,) or tuple(norm_w.shape) != (k,):
+        raise ValueError(f"x and norm_w must be [{k}]")
+    n = blocks.shape[0]
+    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    check("w4a8_gemv_rmsnorm", lib().w4a8_gemv_rmsnorm(blocks.data_ptr(), x.data_ptr(), norm_w.data_ptr(), eps,
+                                                       y.data_ptr(), n, k, _stream(blocks)))
+    return y
+
+
+def gemv_rmsnorm_argmax(blocks, k: int, x, norm_w, eps: float, workspace, out=None):
+    """The LM head step: rmsnorm, Q8_0, GEMV and the greedy pick in one kernel -> (y, argmax)."""
+    import torch
+    _need(x, torch.float32, "x")
+    _need(norm_w, torch.float32, "norm_w")
+    _check_blocks(blocks, k)
+    n = blocks.shape[0]
+    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    best = torch.empty(1, dtype=torch.int32, device=blocks.device)
+    check("w4a8_gemv_rmsnorm_argmax", lib().w4a8_gemv_rmsnorm_argmax(
+        blocks.data_ptr(), x.data_ptr(), norm_w.data_ptr(), eps, y.data_ptr(), n, k, best.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(blocks)))
+    return y, best
+
+
+def gemv_silu_mul(blocks, k: int, gate_up, out=None):
+    """y = W Q8_0(silu(gate) * up) with gate_up = gate | up, float32 [2k], in one kernel."""
+    import torch
+    _need(gate_up, torch.float32, "gate_up")
+    _check_blocks(blocks, k)
+    if tuple(gate_up.shape) != (2 * k,):
+        raise ValueError(f"gate_up must be [{2 * k}]")
+    n = blocks.shape[0]
+    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    check("w4a8_gemv_silu_mul", lib().w4a8_gemv_silu_mul(blocks.data_ptr(), gate_up.data_ptr(), y.data_ptr(), n, k,
+                                                         _stream(blocks)))
+    return y
+
+
+def rmsnorm_q8_0_engine(x, norm_w, eps: float):
+    """Engine-layout rows of Q8_0(rmsnorm(x) * norm_w) for x float32 [k] or [m, k]."""
+    import torch
+    _need(x, torch.float32, "x")
+    _need(norm_w, torch.float32, "norm_w")
+    k = x.shape[-1]
+    m = 1 if x.dim() == 1 else x.shape[0]
+    out = torch.empty((m, k + k // 8), dtype=torch.uint8, device=x.device)
+    check("w4a8_rmsnorm_q8_0", lib().w4a8_rmsnorm_q8_0(x.data_ptr(), norm_w.data_ptr(), eps, out.data_ptr(), k, m,
+                                                       _stream(x)))
+    return out if x.dim() == 2 else out[0]
+
+
+def silu_mul_q8_0_engine(gate_up):
+    """Engine-layout rows of Q8_0(silu(gate) * up) for gate_up float32 [2k] or [m, 2k]."""
+    import torch
+    _need(gate_up, torch.float32, "gate_up")
+    k = gate_up.shape[-1] // 2
+    m = 1 if gate_up.dim() == 1 else gate_up.shape[0]
+    out = torch.empty((m, k + k // 8), dtype=torch.uint8, device=gate_up.device)
+    check("w4a8_silu_mul_q8_0", lib().w4a8_silu_mul_q8_0(gate_up.data_ptr(), out.data_ptr(), k, m, _stream(gate_up)))
+    return out if gate_up.dim() == 2 else out[0]
 
 
 def gemv_q8_0_blocks(blocks, k: int, x_blocks, out=None):

@@ -45,6 +45,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_gemm_q4_0.argtypes = [p, p, p, p, i64, i64, i64, c_int]
         L.oracle_pack_x_for_engine.argtypes = [p, p, p, i64]
         L.oracle_contract_version.restype = ctypes.c_char_p
+        L.oracle_rmsnorm.argtypes = [p, p, i64, ctypes.c_float, p]
+        L.oracle_ggml_expf.argtypes = [ctypes.c_float]
+        L.oracle_ggml_expf.restype = ctypes.c_float
+        L.oracle_silu_mul.argtypes = [p, p, i64, p]
         _lib = L
     return _lib
 
@@ -124,3 +128,27 @@ def pack_x_for_engine(xq: np.ndarray, xd: np.ndarray) -> np.ndarray:
 
 def contract_version() -> str:
     return lib().oracle_contract_version().decode()
+
+
+# ------------------------------------------------ producers of the activation
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """board/tp/tp_llama.cpp:557-569 on float32 [n] (n % 4 == 0)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().oracle_rmsnorm(x.ctypes.data, w.ctypes.data, x.size, float(eps), out.ctypes.data)
+    return out
+
+
+def ggml_expf(x) -> np.float32:
+    return np.float32(lib().oracle_ggml_expf(float(x)))
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """board/tp/tp_llama.cpp:612-619 on float32 [n]."""
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.empty_like(g)
+    lib().oracle_silu_mul(g.ctypes.data, u.ctypes.data, g.size, out.ctypes.data)
+    return out

@@ -192,4 +192,64 @@ void oracle_pack_x_for_engine(const int8_t *xq, const uint16_t *xd16, uint8_t *o
     }
 }
 
+/* ----------------------------------------------- producers of the activation
+ *
+ * The reference's decode loop computes the GEMV inputs with these
+ * (board/tp/tp_llama.cpp); restated in scalar C, one element at a time, in the
+ * same operation order and with the same fused steps. */
+
+/* rmsnorm, tp_llama.cpp:557-569: the sum of squares in float64 in four lanes
+ * (element i in lane i % 4, increasing i; float products are exact in
+ * float64, so the NEON fused multiply-add is the add), met as
+ * (l0 + l2) + (l1 + l3); scale = 1 / sqrtf((float)(ss / n) + eps); out =
+ * (x * scale) * w. n % 4 == 0. */
+void oracle_rmsnorm(const float *x, const float *w, int64_t n, float eps, float *out) {
+    double lane[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int64_t i = 0; i < n; ++i) {
+        const double v = (double)x[i];
+        lane[i & 3] = lane[i & 3] + v * v;
+    }
+    const double ss = (lane[0] + lane[2]) + (lane[1] + lane[3]);
+    const float scale = 1.0f / sqrtf((float)(ss / (double)n) + eps);
+    for (int64_t i = 0; i < n; ++i) {
+        const float a = x[i] * scale;
+        out[i] = a * w[i];
+    }
+}
+
+/* ggml's vector expf (tp_llama.cpp:530-553; Arm optimized-routines, MIT) for
+ * one element: the same constants, order and fused steps (fmaf = the NEON
+ * vfma / vfms). */
+float oracle_ggml_expf(float x) {
+    const float shift = 0x1.8p23f;
+    const float z = fmaf(x, 0x1.715476p+0f, shift);
+    const float n = z - shift;
+    const float b = fmaf(-n, 0x1.7f7d1cp-20f, fmaf(-n, 0x1.62e4p-1f, x));
+    uint32_t zb;
+    memcpy(&zb, &z, 4);
+    const uint32_t e = zb << 23;
+    const uint32_t kb = e + 0x3f800000u;
+    float k;
+    memcpy(&k, &kb, 4);
+    const float u = b * b;
+    const float j = fmaf(fmaf(fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u, fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
+                         u, 0x1.ffffecp-1f * b);
+    if (!(fabsf(n) > 126.0f)) return fmaf(k, j, k);
+    const uint32_t d = n <= 0.0f ? 0x82000000u : 0u;
+    const uint32_t s1b = d + 0x7f000000u, s2b = e - d;
+    float s1, s2;
+    memcpy(&s1, &s1b, 4);
+    memcpy(&s2, &s2b, 4);
+    if (fabsf(n) > 192.0f) return s1 * s1;
+    return fmaf(s2, j, s2) * s1;
+}
+
+/* silu_mul, tp_llama.cpp:612-619: a = (g / (1 + exp(-g))) * u. */
+void oracle_silu_mul(const float *g, const float *u, int64_t n, float *out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float sg = g[i] / (1.0f + oracle_ggml_expf(-g[i]));
+        out[i] = sg * u[i];
+    }
+}
+
 const char *oracle_contract_version(void) { return "llm-kv260/w4a8-q4_0-v2"; }

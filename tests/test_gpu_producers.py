@@ -1,0 +1,99 @@
+"""The reference's activation producers on the GPU, byte for byte against the
+oracle: rmsnorm (board/tp/tp_llama.cpp:557-569) and silu(gate) * up
+(:612-619, ggml's vector expf), each standalone (to the engine layout) and
+fused into the GEMV's activation staging, and the LM head's whole step
+(rmsnorm, Q8_0, GEMV, greedy pick) in one kernel. The inputs include the
+constructed float64-order cases that pin the oracle's rmsnorm and the
+expf's scaling branches (|n| > 126, |n| > 192, overflow)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import c_oracle as C
+import q4_0_oracle as O
+from gpu_helpers import assert_bytes_equal, dev, host
+from test_gpu_argmax import scan_argmax
+from test_oracle_producers import _order_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _engine(h):
+    xq, xd = C.quantize_q8_0(h)
+    return C.pack_x_for_engine(xq, xd)
+
+
+def _gate_up(k, seed):
+    rng = np.random.default_rng(seed)
+    gu = (rng.standard_normal(2 * k) * 4).astype(np.float32)
+    edges = np.array([0.0, -0.0, 100.0, -100.0, 90.0, -90.0, 130.0, -130.0, 200.0, -200.0, 1e-30, 88.7, -88.7],
+                     np.float32)
+    gu[:edges.size] = edges                            # gate edges (their up values are random)
+    return gu
+
+
+@pytest.mark.parametrize("k,m", [(256, 1), (2048, 3), (8192, 2), (16384, 1)])
+def test_rmsnorm_q8_0(gpu, k, m):
+    rng = np.random.default_rng(k + m)
+    x = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    w = rng.standard_normal(k).astype(np.float32)
+    got = host(gpu.rmsnorm_q8_0_engine(dev(x), dev(w), 1e-5))
+    want = np.stack([_engine(C.rmsnorm(x[i], w, 1e-5)) for i in range(m)])
+    assert_bytes_equal(got, want, "rmsnorm_q8_0")
+
+
+@pytest.mark.parametrize("k,m", [(256, 1), (8192, 2), (2048, 5)])
+def test_silu_mul_q8_0(gpu, k, m):
+    gu = np.stack([_gate_up(k, 10 * k + i) for i in range(m)])
+    got = host(gpu.silu_mul_q8_0_engine(dev(gu)))
+    want = np.stack([_engine(C.silu_mul(gu[i, :k], gu[i, k:])) for i in range(m)])
+    assert_bytes_equal(got, want, "silu_mul_q8_0")
+
+
+@pytest.mark.parametrize("rows,k", [(3072, 2048), (100, 256), (512, 8192), (64, 16384), (16384, 2048)])
+def test_gemv_rmsnorm(gpu, rows, k):
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 70 + rows, 0.02))
+    rng = np.random.default_rng(rows)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    w = rng.standard_normal(k).astype(np.float32)
+    xq, xd = C.quantize_q8_0(C.rmsnorm(x, w, 1e-5))
+    y = host(gpu.gemv_rmsnorm(dev(blocks), k, dev(x), dev(w), 1e-5))
+    assert_bytes_equal(y, C.gemv_q4_0(blocks, k, xq, xd), f"gemv_rmsnorm {rows}x{k}")
+
+
+@pytest.mark.parametrize("case", [{1: 512, 2: 512, 3: 512}, {0: 511}, {1: 2, 3: 2}])
+def test_gemv_rmsnorm_float64_order_cases(gpu, case):
+    k = 2048
+    blocks = C.quantize_q4_0(O.normal_f32((256, k), 91, 0.02))
+    x = _order_case(case)
+    w = np.ones(k, np.float32)
+    xq, xd = C.quantize_q8_0(C.rmsnorm(x, w, 0.0))
+    y = host(gpu.gemv_rmsnorm(dev(blocks), k, dev(x), dev(w), 0.0))
+    assert_bytes_equal(y, C.gemv_q4_0(blocks, k, xq, xd), f"order case {case}")
+
+
+@pytest.mark.parametrize("rows,k", [(2048, 8192), (64, 256), (300, 2048)])
+def test_gemv_silu_mul(gpu, rows, k):
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 80 + rows, 0.02))
+    gu = _gate_up(k, rows)
+    xq, xd = C.quantize_q8_0(C.silu_mul(gu[:k], gu[k:]))
+    y = host(gpu.gemv_silu_mul(dev(blocks), k, dev(gu)))
+    assert_bytes_equal(y, C.gemv_q4_0(blocks, k, xq, xd), f"gemv_silu_mul {rows}x{k}")
+
+
+def test_lm_head_step(gpu):
+    """rmsnorm(x, output_norm) -> Q8_0 -> LM head GEMV -> argmax (tp_llama.cpp:878-880), one kernel."""
+    rows, k = 128256, 2048
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 95, 0.02))
+    ws = gpu.argmax_workspace()
+    for seed in (96, 97):
+        rng = np.random.default_rng(seed)
+        x = (rng.standard_normal(k) * 2).astype(np.float32)
+        w = rng.standard_normal(k).astype(np.float32)
+        xq, xd = C.quantize_q8_0(C.rmsnorm(x, w, 1e-5))
+        want = C.gemv_q4_0(blocks, k, xq, xd)
+        y, best = gpu.gemv_rmsnorm_argmax(dev(blocks), k, dev(x), dev(w), 1e-5, ws)
+        assert_bytes_equal(host(y), want, "lm head step")
+        assert int(host(best)[0]) == scan_argmax(want)
