@@ -174,6 +174,99 @@ def time_lm_argmax(torch, kv, cf, stream):
             "argmax": int(best.cpu()[0]), "weight_copies": 3}
 
 
+def time_producers(torch, kv, cf, stream):
+    """us per GEMV with its producer fused into the activation staging (rmsnorm
+    before q|k|v, gate|up and the LM head; silu(gate) * up before down), next to
+    the same work as two launches (standalone producer + engine-layout GEMV)
+    and the plain fp32 GEMV; weights rotated as for the per-shape GEMVs."""
+    L = kv.lib()
+    out = {}
+    ws = kv.argmax_workspace()
+    best = torch.empty(1, dtype=torch.int32, device="cuda")
+    cases = (("qkv_rmsnorm", cf.LAYER_SHAPES[0], "rms"), ("gate_up_rmsnorm", cf.LAYER_SHAPES[2], "rms"),
+             ("down_silu_mul", cf.LAYER_SHAPES[3], "silu"), ("lm_head_rmsnorm_argmax", cf.LM_HEAD, "rms_argmax"))
+    for name, m, kind in cases:
+        base = device_weights(torch, kv, m.rows, m.k, 9)
+        copies = 3 if m.weight_bytes > (100 << 20) else max(3, -(-ROTATE_BYTES // m.weight_bytes))
+        mats = [base] + [base.clone() for _ in range(copies - 1)]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(5)
+        xin = torch.randn(2 * m.k if kind == "silu" else m.k, generator=g, device="cuda")
+        norm = torch.randn(m.k, generator=g, device="cuda")
+        xe = torch.empty(m.k + m.k // 8, dtype=torch.uint8, device="cuda")
+        y = torch.empty(m.rows, dtype=torch.float32, device="cuda")
+        launches = max(copies, 30)
+
+        def fused(w, s):
+            if kind == "silu":
+                return L.w4a8_gemv_silu_mul(w.data_ptr(), xin.data_ptr(), y.data_ptr(), m.rows, m.k, s)
+            if kind == "rms":
+                return L.w4a8_gemv_rmsnorm(w.data_ptr(), xin.data_ptr(), norm.data_ptr(), 1e-5, y.data_ptr(),
+                                           m.rows, m.k, s)
+            return L.w4a8_gemv_rmsnorm_argmax(w.data_ptr(), xin.data_ptr(), norm.data_ptr(), 1e-5, y.data_ptr(),
+                                              m.rows, m.k, best.data_ptr(), ws.data_ptr(), ws.numel(), s)
+
+        def split(w, s):
+            st = (L.w4a8_silu_mul_q8_0(xin.data_ptr(), xe.data_ptr(), m.k, 1, s) if kind == "silu" else
+                  L.w4a8_rmsnorm_q8_0(xin.data_ptr(), norm.data_ptr(), 1e-5, xe.data_ptr(), m.k, 1, s))
+            return st or L.w4a8_gemv(w.data_ptr(), xe.data_ptr(), y.data_ptr(), m.rows, m.k, s)
+
+        r = {"shape": f"{m.rows}x{m.k}"}
+        for label, fn in (("fused_us", fused), ("two_launches_us", split)):
+            calls = [(lambda w: (lambda st: kv.check(name, fn(w, st))))(mats[i % copies]) for i in range(launches)]
+            gr = graph_of(torch, stream, calls)
+            ms, _ = time_replays(torch, stream, gr, 10, 2)
+            r[label] = round(ms * 1e3 / launches, 3)
+            del gr
+        out[name] = r
+        del mats, base
+        torch.cuda.empty_cache()
+    return out
+
+
+def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup):
+    """The decode step with its producers fused and its one in-step data
+    dependency kept: per layer q|k|v = W rmsnorm(x), o = W x, gate|up =
+    W rmsnorm(x), down = W (silu(gate) * up) of gate|up's own output; the LM
+    head = W rmsnorm(x) with its greedy pick. The rmsnorm inputs (the residual
+    stream) and o's input (the attention output) are seeded vectors: attention
+    and the residual adds are not part of the engine."""
+    L = kv.lib()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    k = cf.LAYER_SHAPES[0].k
+    resid = torch.randn(k, generator=g, device="cuda")
+    attn = torch.randn(k, generator=g, device="cuda")
+    norm = torch.randn(k, generator=g, device="cuda")
+    ws = kv.argmax_workspace()
+    best = torch.empty(1, dtype=torch.int32, device="cuda")
+    calls = []
+    for i, m in enumerate(chain):
+        w, y = mats[i], ys[i]
+        role = "lm" if i == len(chain) - 1 else ("qkv", "o", "gate_up", "down")[i % 4]
+        if role in ("qkv", "gate_up"):
+            calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_rmsnorm(w.data_ptr(), resid.data_ptr(), norm.data_ptr(),
+                                                                        1e-5, y.data_ptr(), m.rows, m.k, s))(w, y, m))
+        elif role == "o":
+            calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_f32(w.data_ptr(), attn.data_ptr(), y.data_ptr(),
+                                                                    m.rows, m.k, s))(w, y, m))
+        elif role == "down":
+            gu = ys[i - 1]
+            calls.append((lambda w, y, m, gu: lambda s: L.w4a8_gemv_silu_mul(w.data_ptr(), gu.data_ptr(), y.data_ptr(),
+                                                                             m.rows, m.k, s))(w, y, m, gu))
+        else:
+            calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_rmsnorm_argmax(
+                w.data_ptr(), resid.data_ptr(), norm.data_ptr(), 1e-5, y.data_ptr(), m.rows, m.k, best.data_ptr(),
+                ws.data_ptr(), ws.numel(), s))(w, y, m))
+    checked = [(lambda c: lambda s: kv.check("fused chain", c(s)))(c) for c in calls]
+    gr = graph_of(torch, stream, checked)
+    ms, _ = time_replays(torch, stream, gr, steps, warmup)
+    del gr
+    return {"us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "launches_per_step": len(calls),
+            "gbps": round(cf.chain_algorithmic_bytes() / (ms * 1e-3) / 1e9, 1),
+            "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
+
+
 def time_gemm(torch, kv, cf, m, mrows, stream):
     """us per M > 1 GEMM (engine-layout activation rows), rotating weight copies."""
     L = kv.lib()
@@ -295,6 +388,9 @@ def main() -> int:
     batch_gbs = chain_bytes / (ms_batch * 1e-3) / 1e9
     log(f"batch: {ms_batch * 1e3:.1f} us/step, {batch_gbs:.0f} GB/s (one launch, no order inside a step)")
     del g_chain, g_batch
+    fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup)
+    log(f"fused chain: {fused_chain['us_per_step']} us/step, {fused_chain['tokens_per_s']} tokens/s "
+        "(rmsnorm / silu fused, LM head with argmax)")
 
     gemv, gemm = {}, []
     shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES
@@ -310,6 +406,9 @@ def main() -> int:
                 gemm.append(dict(name=m.name, **r))
                 log(f"gemm {m.name} M={mrows}: {r['us']} us, {r['gbps']} GB/s, {r['tops']} TOP/s")
             torch.cuda.empty_cache()
+    producers = {} if args.no_gemv else time_producers(torch, kv, cf, stream)
+    for name, r in producers.items():
+        log(f"producer {name} {r['shape']}: fused {r['fused_us']} us, two launches {r['two_launches_us']} us")
     lm_argmax = time_lm_argmax(torch, kv, cf, stream)
     log(f"gemv lm_head + argmax: {lm_argmax['us']} us, {lm_argmax['gbps']} GB/s")
     lm = gemv["lm_head"]
@@ -367,6 +466,8 @@ def main() -> int:
         "gemv": gemv,
         "gemm": gemm,
         "lm_head_argmax": lm_argmax,
+        "producers": producers,
+        "chain_fused_producers": fused_chain,
         "caller": caller,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),

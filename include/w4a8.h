@@ -93,7 +93,10 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
  *     float32[2k] (the gate|up GEMV's output), silu(g) = g / (1 + expf(-g))
  *     through ggml's vector expf; the input of down (:858-860). y = W Q8_0(a).
  * Each is byte-identical to the standalone producer below followed by
- * w4a8_gemv. x, norm_w and gate_up 16-byte aligned. */
+ * w4a8_gemv. x, norm_w and gate_up 16-byte aligned; the fused rmsnorm takes
+ * k <= 8192 (its float64 squares are staged in LDS), the standalone one any k.
+ * The float64 sum is n / 4 dependent adds whatever the hardware: about 8 ns
+ * each here, the latency the reference's summation order costs. */
 int w4a8_gemv_rmsnorm(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
                       void *stream);
 int w4a8_gemv_rmsnorm_argmax(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,

@@ -92,9 +92,13 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
     return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream, argmax, workspace));
 }
 
+// The fused rmsnorm stages x's float64 squares in LDS: k <= 8192.
+constexpr int RMS_FUSED_MAX_K = 8192;
+
 int w4a8_gemv_rmsnorm(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
                       void *stream) {
     if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    if (k > RMS_FUSED_MAX_K) return W4A8_ERR_SHAPE;
     if (!norm_w) return W4A8_ERR_NULL;
     if (!aligned(norm_w, 16)) return W4A8_ERR_ALIGN;
     XAux aux;
@@ -106,6 +110,7 @@ int w4a8_gemv_rmsnorm(const void *w, const float *x, const float *norm_w, float 
 int w4a8_gemv_rmsnorm_argmax(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
                              int32_t *argmax, void *workspace, size_t workspace_bytes, void *stream) {
     if (int s = check_gemv(w, x, y, rows, k, 16)) return s;
+    if (k > RMS_FUSED_MAX_K) return W4A8_ERR_SHAPE;
     if (!norm_w || !argmax || !workspace) return W4A8_ERR_NULL;
     if (!aligned(norm_w, 16) || !aligned(argmax, 4) || !aligned(workspace, 16)) return W4A8_ERR_ALIGN;
     if (workspace_bytes < argmax_workspace_bytes()) return W4A8_ERR_SHAPE;

@@ -73,11 +73,10 @@ struct GemvParams {
     int tiles;        // ceil(rows / rpw)
     int paired;       // v2 port layout
     // Argmax epilogue (LM head): the first row of the largest y, written to
-    // *argmax by the last workgroup to finish; partials[workgroup] and the
-    // ticket counter live in the caller's workspace (the counter is zero
-    // between calls).
+    // *argmax by the last workgroup to finish; the merged key and the ticket
+    // counter live in the caller's workspace (both zero between calls).
     int32_t *argmax;
-    unsigned long long *partials;
+    unsigned long long *key;
     unsigned int *ticket;
     // X_RMS: the norm weight float32[k] and epsilon.
     const float *norm_w;
@@ -87,11 +86,12 @@ struct GemvParams {
 // Argmax key of y[row] = v: the largest v wins, and among equal values the
 // smallest row, which is the reference's scan (board/tp/tp_llama.cpp:879-880,
 // "if (y[i] > y[best]) best = i"). -0 compares equal to +0 there, so it is
-// keyed as +0; a NaN never compares greater, so it gets key 0 and never wins
-// (a NaN at row 0 is handled by the last workgroup: the scan starts there and
-// then keeps 0). Every other value has key > 0.
+// keyed as +0; a NaN never compares greater, so it gets key 0 and never wins,
+// except at row 0, where the scan starts and then keeps 0: that NaN gets the
+// largest key of all. Every other value has a key in between.
+constexpr unsigned long long ARGMAX_ROW0_NAN = ~0ull;
 __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
-    if (v != v) return 0ull;
+    if (v != v) return row == 0 ? ARGMAX_ROW0_NAN : 0ull;
     const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
     const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)row);
@@ -297,8 +297,8 @@ __device__ __forceinline__ void chunk_terms(const uint32_t w[CHUNK_DWORDS], cons
 }
 
 constexpr int TILE_BYTES = 64 * CHUNK_BYTES;   // 9,216
-// Argmax workspace: the ticket counter in its own 64-byte line, then the partials.
-constexpr size_t ARGMAX_PARTIALS_OFFSET = 64;
+// Argmax workspace: the ticket counter and the merged key, each in its own 64-byte line.
+constexpr size_t ARGMAX_KEY_OFFSET = 64;
 // Tiles per wave held in registers: three for plain matrices; two for the
 // board layouts, whose per-lane address tables take the third's registers.
 template <bool PLAIN>
@@ -356,14 +356,18 @@ __device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t y, int byte_off, 
 
 // ONE_PASS: a tile holds at most eight rows (K >= 2048), so one pass of the
 // ordered sums covers it and each lane stores at most one value per tile.
-// The workgroup's best key (its waves' keys through LDS), published as this
-// workgroup's partial; the last workgroup to arrive reduces all partials,
-// writes the row, and sets the ticket back to zero for the next call.
-__device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long long best, int block, int nblocks,
+// The workgroup's best key (its waves' keys through LDS) goes into the
+// launch's key with one device-scope atomic max; then the workgroup takes a
+// ticket. Both are relaxed atomics performed where every XCD sees them, and
+// the ticket is taken only after the max has returned, so the workgroup that
+// draws the last ticket reads a key every other workgroup has already merged.
+// No fence is needed (an agent-scope release or acquire would write back or
+// invalidate the whole L2 of every XCD in turn). The last workgroup writes the
+// row and clears the key and the ticket for the next call.
+__device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long long best, int nblocks,
                                               uint8_t *lds) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
     unsigned long long *keys = reinterpret_cast<unsigned long long *>(lds);   // the slabs are free by now
-    __shared__ int last;
     best = wave_max_u64(best);
     __syncthreads();
     if (lane == 0) keys[wave] = best;
@@ -371,27 +375,18 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
     if (tid == 0) {
         unsigned long long b = 0;
         for (int w = 0; w < waves; ++w) b = max_u64(b, keys[w]);
-        __hip_atomic_store(&P.partials[block], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned t = __hip_atomic_fetch_add(P.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = t == (unsigned)(nblocks - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __atomic_thread_fence(__ATOMIC_ACQUIRE);
-    unsigned long long b = 0;
-    for (int i = tid; i < nblocks; i += blockDim.x)
-        b = max_u64(b, __hip_atomic_load(&P.partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    b = wave_max_u64(b);
-    __syncthreads();
-    if (lane == 0) keys[wave] = b;
-    __syncthreads();
-    if (tid == 0) {
-        unsigned long long k = 0;
-        for (int w = 0; w < waves; ++w) k = max_u64(k, keys[w]);
-        const float y0 = __hip_atomic_load(&P.y[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int32_t row = (k == 0ull || y0 != y0) ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)k);
-        __hip_atomic_store(P.argmax, row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(P.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long seen = __hip_atomic_fetch_max(P.key, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // The ticket depends on the max's result (no key equals ARGMAX_ROW0_NAN - 1),
+        // so it is taken after the max is done.
+        const unsigned inc = seen == ARGMAX_ROW0_NAN - 1 ? 2u : 1u;
+        const unsigned t = __hip_atomic_fetch_add(P.ticket, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == (unsigned)(nblocks - 1)) {
+            const unsigned long long k = __hip_atomic_load(P.key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int32_t row = (k == 0ull || k == ARGMAX_ROW0_NAN) ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)k);
+            __hip_atomic_store(P.argmax, row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(P.key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(P.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -448,23 +443,30 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     auto stage_x = [&]() {
         float rms = 0.0f;
         if constexpr (XF == X_RMS) {
-            // rmsnorm's scale needs the whole of x: staged as fp32 after the
-            // block sums, reduced by wave 0, handed out through LDS.
-            float *xs = reinterpret_cast<float *>(s_s + nb);
-            float *s_rms = xs + P.k;
-            if (tid < nb) {
+            // rmsnorm's scale needs the whole of x: its squares go to LDS as
+            // float64 after the block sums, wave 0 reduces them, and the
+            // scale comes back through LDS.
+            double *sq = reinterpret_cast<double *>(s_s + nb);
+            float *s_rms = reinterpret_cast<float *>(sq + P.k);
+            auto squares = [&](const XRaw<XF> &r, int b) {
 #pragma unroll
-                for (int m = 0; m < 8; ++m) reinterpret_cast<float4 *>(xs + 32 * tid)[m] = xr.v[m];
-            }
+                for (int m = 0; m < 8; ++m) {
+                    const double a = r.v[m].x, c = r.v[m].y, d = r.v[m].z, e = r.v[m].w;
+                    sq[32 * b + 4 * m] = a * a;
+                    sq[32 * b + 4 * m + 1] = c * c;
+                    sq[32 * b + 4 * m + 2] = d * d;
+                    sq[32 * b + 4 * m + 3] = e * e;
+                }
+            };
+            if (tid < nb) squares(xr, tid);
             for (int b = tid + nthreads; b < nb; b += nthreads) {
                 XRaw<XF> xb;
                 x_load<XF>(P.x, P.k, b, true, xb, P.norm_w);
-#pragma unroll
-                for (int m = 0; m < 8; ++m) reinterpret_cast<float4 *>(xs + 32 * b)[m] = xb.v[m];
+                squares(xb, b);
             }
             __syncthreads();
             if (wave == 0) {
-                const float sc = rms_scale_wave(xs, P.k, P.eps);
+                const float sc = rms_scale_wave(sq, P.k, P.eps);
                 if (lane == 0) *s_rms = sc;
             }
             __syncthreads();
@@ -591,7 +593,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     } else {
         stage_x();
     }
-    if constexpr (ARGMAX) argmax_finish(P, best, block, nblocks, lds);
+    if constexpr (ARGMAX) argmax_finish(P, best, nblocks, lds);
 }
 
 template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false>
@@ -688,7 +690,7 @@ int device_cu_count() {
     return cached[dev];
 }
 
-size_t argmax_workspace_bytes() { return ARGMAX_PARTIALS_OFFSET + 8 * (size_t)(2 * device_cu_count()); }
+size_t argmax_workspace_bytes() { return ARGMAX_KEY_OFFSET + 64; }
 
 hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *y, hipStream_t stream,
                           int32_t *argmax, void *workspace, XAux aux) {
@@ -698,7 +700,7 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     if (argmax) {
         P.argmax = argmax;
         P.ticket = static_cast<unsigned int *>(workspace);
-        P.partials = reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(workspace) + ARGMAX_PARTIALS_OFFSET);
+        P.key = reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(workspace) + ARGMAX_KEY_OFFSET);
     }
     for (int s = 0; s < 4; ++s) P.seg[s] = s < w.nseg ? w.seg[s] : w.seg[0];
     P.x = x;
@@ -717,8 +719,9 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     const int cus = device_cu_count();
     const int nb = w.k / QK;
     // Staged activation: int8 values, fp32 scale and int32 sum per block; for
-    // X_RMS also x itself as fp32 and the rmsnorm scale.
-    const size_t x_lds = (size_t)nb * 40 + (xf == X_RMS ? (size_t)w.k * 4 + 16 : 0);
+    // X_RMS also the squares of x as float64 and the rmsnorm scale.
+    if (xf == X_RMS && w.k > 8192) return hipErrorInvalidValue;
+    const size_t x_lds = (size_t)nb * 40 + (xf == X_RMS ? (size_t)w.k * 8 + 16 : 0);
     // Small matrices: one tile per wave, workgroups spread over every CU
     // (each stages its own copy of x in parallel). Larger ones: at most eight
     // waves per CU (the register budget of three tiles per wave allows two
@@ -742,8 +745,6 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     const int threads = 64 * waves;
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
     if (argmax) {
-        // The workspace holds one partial per workgroup: at most two per CU.
-        if (grid > 2 * cus) return hipErrorInvalidValue;
         if (xf == X_F32) return launch_layout<X_F32, true>(P, plain, grid, threads, lds, stream);
         if (xf == X_RMS) return launch_layout<X_RMS, true>(P, plain, grid, threads, lds, stream);
         return hipErrorInvalidValue;

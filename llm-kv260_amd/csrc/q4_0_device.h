@@ -156,19 +156,32 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return sg * u;
 }
 
-// rmsnorm's scale (tp_llama.cpp:557-569) over x[0..n) in LDS, n % 4 == 0: the
-// sum of squares accumulates in float64 in four lanes, element i in lane i % 4
-// in increasing i; the lanes meet as (l0 + l2) + (l1 + l3); then
-// 1 / sqrtf((float)(ss / n) + eps). Lanes 0..3 of the calling wave do the
-// four chains; the result is returned in every lane of the wave.
-__device__ __forceinline__ float rms_scale_wave(const float *xs, int n, float eps) {
+// rmsnorm's scale (tp_llama.cpp:557-569) from sq[i] = (double)x[i]^2 in LDS
+// (exact: a float32 square fits a float64), n % 128 == 0: the sum of squares
+// accumulates in float64 in four lanes, element i in lane i % 4 in increasing
+// i (the reference's fused multiply-add of an exact square is this add); the
+// lanes meet as (l0 + l2) + (l1 + l3); then 1 / sqrtf((float)(ss / n) + eps).
+// Lanes 0..3 of the calling wave run the four chains of n / 4 dependent adds,
+// the next B squares read while the current B are added; the result is
+// returned in every lane of the wave. The squares are written by the whole
+// workgroup beforehand, so the chains carry the adds and nothing else.
+__device__ __forceinline__ float rms_scale_wave(const double *sq, int n, float eps) {
     const int lane = threadIdx.x & 63;
     double acc = 0.0;
     if (lane < 4) {
-#pragma unroll 8
-        for (int i = lane; i < n; i += 4) {
-            const double v = (double)xs[i];
-            acc = acc + v * v;
+        constexpr int B = 8;
+        double cur[B], nxt[B];
+#pragma unroll
+        for (int t = 0; t < B; ++t) cur[t] = sq[lane + 4 * t];
+        for (int base = 0; base < n; base += 4 * B) {
+            // The last pass reads the first squares again (in range, unused).
+            const int next = base + 4 * B < n ? base + 4 * B : 0;
+#pragma unroll
+            for (int t = 0; t < B; ++t) nxt[t] = sq[next + lane + 4 * t];
+#pragma unroll
+            for (int t = 0; t < B; ++t) acc = acc + cur[t];
+#pragma unroll
+            for (int t = 0; t < B; ++t) cur[t] = nxt[t];
         }
     }
     const double l1 = __shfl(acc, 1), l2 = __shfl(acc, 2), l3 = __shfl(acc, 3), l0 = __shfl(acc, 0);

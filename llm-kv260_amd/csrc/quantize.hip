@@ -88,28 +88,36 @@ __global__ __launch_bounds__(256) void silu_mul_q8_0_kernel(const float *__restr
 
 // h = rmsnorm(x) * norm_w (tp_llama.cpp:557-569) of m rows of float32[k],
 // quantized to the engine layout: one workgroup per row (the sum of squares
-// runs over the whole row), x staged in LDS for wave 0's four fp64 chains.
+// runs over the whole row); the squares in LDS as float64 for wave 0's four
+// chains, x read again (from L2) for the normalization.
 __global__ __launch_bounds__(256) void rmsnorm_q8_0_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                            float eps, int k, uint8_t *__restrict__ out) {
-    extern __shared__ __attribute__((aligned(16))) float xs[];
+    extern __shared__ __attribute__((aligned(16))) double sq[];
     __shared__ float scale;
     const int row = blockIdx.x, nb = k >> 5;
     const float *xr = x + (size_t)row * k;
-    for (int i = threadIdx.x; i < k / 4; i += blockDim.x)
-        reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(xr)[i];
+    for (int i = threadIdx.x; i < k / 4; i += blockDim.x) {
+        const float4 v = reinterpret_cast<const float4 *>(xr)[i];
+        const double a = v.x, b = v.y, c = v.z, d = v.w;
+        sq[4 * i] = a * a;
+        sq[4 * i + 1] = b * b;
+        sq[4 * i + 2] = c * c;
+        sq[4 * i + 3] = d * d;
+    }
     __syncthreads();
     if (threadIdx.x < 64) {
-        const float sc = rms_scale_wave(xs, k, eps);
+        const float sc = rms_scale_wave(sq, k, eps);
         if (threadIdx.x == 0) scale = sc;
     }
     __syncthreads();
     const float sc = scale;
     for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-        float wv[32], v[32];
+        float xv[32], wv[32], v[32];
+        load_block(xr + 32 * b, xv);
         load_block(w + 32 * b, wv);
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
-            const float a = xs[32 * b + e] * sc;
+            const float a = xv[e] * sc;
             v[e] = a * wv[e];
         }
         quantize_store<X_ENGINE>(v, row, b, k, out);
@@ -177,11 +185,11 @@ hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out
 hipError_t launch_rmsnorm_q8_0(const float *x, const float *w, float eps, int k, int m, uint8_t *out,
                                hipStream_t stream) {
     if (m <= 0) return hipSuccess;
-    const size_t lds = (size_t)k * 4;
+    const size_t lds = (size_t)k * 8;                       // float64 squares: 128 KB at k = 16384
     static bool lds_allowed = false;
     if (!lds_allowed) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&rmsnorm_q8_0_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
         if (e != hipSuccess) return e;
         lds_allowed = true;
     }

@@ -52,7 +52,7 @@ def test_silu_mul_q8_0(gpu, k, m):
     assert_bytes_equal(got, want, "silu_mul_q8_0")
 
 
-@pytest.mark.parametrize("rows,k", [(3072, 2048), (100, 256), (512, 8192), (64, 16384), (16384, 2048)])
+@pytest.mark.parametrize("rows,k", [(3072, 2048), (100, 256), (512, 8192), (16384, 2048), (40, 768)])
 def test_gemv_rmsnorm(gpu, rows, k):
     blocks = C.quantize_q4_0(O.normal_f32((rows, k), 70 + rows, 0.02))
     rng = np.random.default_rng(rows)
@@ -61,6 +61,15 @@ def test_gemv_rmsnorm(gpu, rows, k):
     xq, xd = C.quantize_q8_0(C.rmsnorm(x, w, 1e-5))
     y = host(gpu.gemv_rmsnorm(dev(blocks), k, dev(x), dev(w), 1e-5))
     assert_bytes_equal(y, C.gemv_q4_0(blocks, k, xq, xd), f"gemv_rmsnorm {rows}x{k}")
+
+
+def test_gemv_rmsnorm_rejects_k_past_8192(gpu):
+    k = 16384
+    blocks = dev(C.quantize_q4_0(O.normal_f32((16, k), 1, 0.02)))
+    x = dev(O.normal_f32((1, k), 2)[0])
+    with pytest.raises(gpu.W4A8Error) as e:
+        gpu.gemv_rmsnorm(blocks, k, x, x, 1e-5)
+    assert e.value.status == -2
 
 
 @pytest.mark.parametrize("case", [{1: 512, 2: 512, 3: 512}, {0: 511}, {1: 2, 3: 2}])
