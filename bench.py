@@ -267,6 +267,31 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup):
             "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
 
 
+def time_prefill(torch, kv, cf, chain, mats, stream, mrows, reps=5):
+    """A prompt of mrows tokens through the step's 65 matrices at once: per matrix
+    one Q8_0 quantize of the mrows float32 activation rows and one M > 1 GEMM
+    (int8 MFMA), in order, from a HIP graph. The reference prefills one decode
+    pass per token (docs/buildlog/0008-openai-api.md:73-74)."""
+    L = kv.lib()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    calls, keep = [], []
+    for i, m in enumerate(chain):
+        x = torch.randn((mrows, m.k), generator=g, device="cuda")
+        xe = torch.empty((mrows, m.k + m.k // 8), dtype=torch.uint8, device="cuda")
+        y = torch.empty((mrows, m.rows), dtype=torch.float32, device="cuda")
+        keep += [x, xe, y]
+        calls.append((lambda w, x, xe, y, m: lambda s: kv.check("prefill", L.w4a8_quantize_q8_0(
+            x.data_ptr(), xe.data_ptr(), m.k, mrows, s) or L.w4a8_gemm(w.data_ptr(), xe.data_ptr(), y.data_ptr(),
+                                                                      mrows, m.rows, m.k, s)))(mats[i], x, xe, y, m))
+    gr = graph_of(torch, stream, calls)
+    ms, _ = time_replays(torch, stream, gr, reps, 1)
+    del gr, keep
+    torch.cuda.empty_cache()
+    return {"tokens": mrows, "ms_per_prompt": round(ms, 4), "tokens_per_s": round(mrows / (ms * 1e-3), 1),
+            "launches": 2 * len(chain)}
+
+
 def time_gemm(torch, kv, cf, m, mrows, stream):
     """us per M > 1 GEMM (engine-layout activation rows), rotating weight copies."""
     L = kv.lib()
@@ -296,7 +321,9 @@ def run_caller(tokens=20):
     import subprocess
     out = {}
     for name, extra in (("gemv2", []), ("v1", ["--v1"])):
-        p = subprocess.run([CALLER, "--tokens", str(tokens), *extra], capture_output=True, text=True, timeout=300)
+        env = dict(os.environ, KV260GEMV_UDMABUF_SIZES="udmabuf0=1G")
+        p = subprocess.run([CALLER, "--tokens", str(tokens), *extra], capture_output=True, text=True, timeout=300,
+                           env=env)
         if p.returncode != 0:
             raise RuntimeError(f"engine_caller {name} failed: {p.stderr[-500:]}")
         out[name] = json.loads(p.stdout.strip().splitlines()[-1])
@@ -345,6 +372,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the per-shape GEMV and GEMM timings")
+    ap.add_argument("--no-caller", action="store_true", help="skip the reference-ABI caller (a child process)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first copy MB of device memory once: a plain copy of known size whose "
                          "FETCH_SIZE / WRITE_SIZE counters scale the kernels' HBM traffic")
@@ -388,6 +416,10 @@ def main() -> int:
     batch_gbs = chain_bytes / (ms_batch * 1e-3) / 1e9
     log(f"batch: {ms_batch * 1e3:.1f} us/step, {batch_gbs:.0f} GB/s (one launch, no order inside a step)")
     del g_chain, g_batch
+    prefill = [time_prefill(torch, kv, cf, chain, mats, stream, mr) for mr in (24, 64)]
+    for r in prefill:
+        log(f"prefill {r['tokens']} tokens: {r['ms_per_prompt']} ms, {r['tokens_per_s']} tokens/s "
+            f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token)")
     fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup)
     log(f"fused chain: {fused_chain['us_per_step']} us/step, {fused_chain['tokens_per_s']} tokens/s "
         "(rmsnorm / silu fused, LM head with argmax)")
@@ -415,9 +447,11 @@ def main() -> int:
     lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 
     traffic = pmc_traffic() or {}
-    log("the reference's caller through the reference ABI (host-visible)")
-    caller = run_caller()
-    for name, r in caller.items():
+    caller = None
+    if not args.no_caller:
+        log("the reference's caller through the reference ABI (host-visible)")
+        caller = run_caller()
+    for name, r in (caller or {}).items():
         log(f"caller {name}: {r['ms_per_token']:.3f} ms/token, {r['us_per_call']['total']:.1f} us/call host-visible")
     cpu = None
     if not args.no_cpu:
@@ -468,6 +502,7 @@ def main() -> int:
         "lm_head_argmax": lm_argmax,
         "producers": producers,
         "chain_fused_producers": fused_chain,
+        "prefill": prefill,
         "caller": caller,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),

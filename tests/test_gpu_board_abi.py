@@ -38,6 +38,7 @@ u64, i32, vp = ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p
 
 @pytest.fixture(scope="module")
 def board(gpu):
+    before = os.environ.get("KV260GEMV_UDMABUF_SIZES")
     os.environ["KV260GEMV_UDMABUF_SIZES"] = "udmabuf0=96M"
     L = gpu.lib()
     L.udmabuf_open.argtypes = [ctypes.POINTER(Udmabuf), ctypes.c_char_p]
@@ -60,6 +61,10 @@ def board(gpu):
     assert L.udmabuf_open(ctypes.byref(pool), b"udmabuf0") == 0
     yield L, pool
     L.udmabuf_close(ctypes.byref(pool))
+    if before is None:
+        os.environ.pop("KV260GEMV_UDMABUF_SIZES", None)
+    else:
+        os.environ["KV260GEMV_UDMABUF_SIZES"] = before
 
 
 def _alloc(L, pool, data_or_size, align=4096):

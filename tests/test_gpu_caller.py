@@ -32,7 +32,8 @@ def _run(tmp_path, *args):
     dump = tmp_path / "dump"
     dump.mkdir()
     print(f"engine_caller {' '.join(args)}", flush=True)
-    p = subprocess.run([CALLER, *args, "--dump", str(dump)], capture_output=True, text=True, timeout=180)
+    env = dict(os.environ, KV260GEMV_UDMABUF_SIZES="udmabuf0=1G")    # the caller's own pool, whatever ran before
+    p = subprocess.run([CALLER, *args, "--dump", str(dump)], capture_output=True, text=True, timeout=180, env=env)
     assert p.returncode == 0, p.stderr[-2000:]
     return json.loads(p.stdout.strip().splitlines()[-1]), dump
 
