@@ -10,9 +10,10 @@
 //    21-25 streams). A wave tile is 64 / C whole rows (C = K / 256 chunks per
 //    row), at most 64 chunks = 9,216 contiguous bytes: nine
 //    global_load_dwordx4, lane l loading bytes 1024 p + 16 l of the tile.
-//  * Each wave keeps three tiles in registers: while it computes one, the
-//    next two are in flight, and the one it just consumed is refilled before
-//    its terms are computed (27 KB per wave, 8 waves per CU).
+//  * Each wave keeps two tiles in registers: while it computes one, the next
+//    is in flight, and the one it just consumed is refilled before its terms
+//    are computed (18 KB per wave). Large matrices launch three 4-wave
+//    workgroups per CU, two of them resident at a time.
 //  * A tile's pieces go through a per-wave 9 KB LDS slab (ds_write_b128 in
 //    load order, ds_read_b128 in chunk order), so that lane l ends up with
 //    chunk l: 144 bytes, eight whole blocks.
@@ -109,10 +110,14 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 #define W4A8_BATCH_WAVES 4
 #endif
 #ifndef W4A8_BATCH_TILES_PER_WAVE
-#define W4A8_BATCH_TILES_PER_WAVE 12
+#define W4A8_BATCH_TILES_PER_WAVE 20
 #endif
 constexpr int BATCH_THREADS = 64 * W4A8_BATCH_WAVES;
 constexpr int BATCH_TILES_PER_WAVE = W4A8_BATCH_TILES_PER_WAVE;
+#ifndef W4A8_MID_TILES_PER_WAVE
+#define W4A8_MID_TILES_PER_WAVE 4
+#endif
+constexpr int MID_TILES_PER_WAVE = W4A8_MID_TILES_PER_WAVE;
 
 struct BatchEntry {
     const uint8_t *w;
@@ -299,10 +304,11 @@ __device__ __forceinline__ void chunk_terms(const uint32_t w[CHUNK_DWORDS], cons
 constexpr int TILE_BYTES = 64 * CHUNK_BYTES;   // 9,216
 // Argmax workspace: the ticket counter and the merged key, each in its own 64-byte line.
 constexpr size_t ARGMAX_KEY_OFFSET = 64;
-// Tiles per wave held in registers: three for plain matrices; two for the
-// board layouts, whose per-lane address tables take the third's registers.
+// Tiles per wave held in registers. Two: a third (tried for plain matrices)
+// raised no shape's rate and took 36 VGPRs, and the board layouts' per-lane
+// address tables need those registers anyway.
 template <bool PLAIN>
-constexpr int depth_of() { return PLAIN ? 3 : 2; }
+constexpr int depth_of() { return 2; }
 
 struct Tile {
     u32x4 p[CHUNK_PIECES];
@@ -583,8 +589,9 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) step(buf[d], refill_t{});
         }
-        if (done < n_my) step(buf[0], last_t{});
-        if (done + 1 < n_my) step(buf[1], last_t{});
+#pragma unroll
+        for (int d = 0; d + 1 < DEPTH; ++d)
+            if (done + d < n_my) step(buf[d], last_t{});
     } else if (n_my == 1) {
         Tile b;
         load_tile<PLAIN>(P, tile, lane, dr, col, pc, b);
@@ -624,22 +631,25 @@ __host__ __device__ inline int batch_blocks(int rows, int k, int tiles_per_block
     return (tiles + tiles_per_block - 1) / tiles_per_block;
 }
 
-// Many independent GEMVs in one launch: workgroups [b_j, b_j + n_j) serve
-// entry j (n_j = batch_blocks of its shape), each exactly as the
-// single-matrix kernel would with a grid of n_j workgroups.
+// Many independent GEMVs in one launch: each entry j gets n_j workgroups
+// (n_j = batch_blocks of its shape), each working exactly as the
+// single-matrix kernel would with a grid of n_j workgroups. The entries take
+// the workgroup indices from the last one backwards, so the largest matrix
+// of a decode step (the LM head, listed last) is dispatched first and the
+// small ones fill the end of the launch.
 // Two waves per SIMD (two workgroups per CU), as the single-matrix kernel runs.
 // ONE_PASS: every entry has K >= 2048 (at most eight rows per tile).
 template <bool ONE_PASS>
 __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemv_batch_kernel(BatchParams B) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int b = blockIdx.x;
-    int j = 0, nblk = 0;
-    for (; j < B.n; ++j) {
+    int j = B.n - 1, nblk = 0;
+    for (; j >= 0; --j) {
         nblk = batch_blocks(B.e[j].rows, B.e[j].k, B.tiles_per_block);
         if (b < nblk) break;
         b -= nblk;
     }
-    if (j >= B.n) return;
+    if (j < 0) return;
     GemvParams P;
     derive_plain(P, B.e[j].w, B.e[j].x, B.e[j].y, B.e[j].rows, B.e[j].k);
     gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, lds);
@@ -722,25 +732,47 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     // X_RMS also the squares of x as float64 and the rmsnorm scale.
     if (xf == X_RMS && w.k > 8192) return hipErrorInvalidValue;
     const size_t x_lds = (size_t)nb * 40 + (xf == X_RMS ? (size_t)w.k * 8 + 16 : 0);
-    // Small matrices: one tile per wave, workgroups spread over every CU
-    // (each stages its own copy of x in parallel). Larger ones: at most eight
-    // waves per CU (the register budget of three tiles per wave allows two
-    // waves per SIMD), every wave walking tiles with a stride of the whole
-    // grid. Every shape has at least one thread per activation block, so the
-    // activation is staged in one pass (K / 32 blocks over 64 * waves threads).
+    // Launch shape, from what bounds each size:
+    //  * Small matrices (at most two tiles per CU): latency. One tile per
+    //    wave, workgroups spread over every CU (each stages its own copy of
+    //    x in parallel).
+    //  * Mid-size (up to eight tiles per CU): one workgroup per CU whose waves
+    //    walk up to MID_TILES_PER_WAVE tiles each, so a wave computes one
+    //    tile while the next is still arriving (four per wave rather than one
+    //    took gate|up from 7.2 to 6.7 us; down, at four tiles per CU, keeps
+    //    one per wave for its activation's 256 blocks).
+    //  * Large: bandwidth. Four-wave workgroups, every wave walking tiles
+    //    with a stride of the whole grid, at most eight resident waves per CU
+    //    (two tiles and the activation column take about 208 VGPRs, two
+    //    waves per SIMD); three workgroups per CU (below).
+    // Every workgroup has at least one thread per activation block, so x is
+    // staged in one pass. (Spreading an fp32 x's quantization over 2-8
+    // threads per block, in helper waves or in the spare threads of the
+    // larger workgroups, made no launch faster: the down GEMV lost 0.9 us.)
     const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;     // <= 8 for K <= 16384
     int waves = min_waves;
     int grid = (P.tiles + waves - 1) / waves;
     if (P.tiles > 2 * cus) {
-        // Up to eight tiles per CU: one workgroup per CU with a wave per tile.
-        // More: two workgroups of four waves per CU (the faster shape when
-        // every wave walks several tiles).
-        const bool many = P.tiles > 8 * cus;
-        const int per_cu = many ? 2 : 1;
-        waves = many ? 4 : (P.tiles + cus - 1) / cus;
-        if (waves < min_waves) waves = min_waves;
-        grid = (P.tiles + waves - 1) / waves;
-        if (grid > cus * per_cu) grid = cus * per_cu;
+        if (P.tiles > 8 * cus) {
+            // Three workgroups per CU: two are resident at a time and the
+            // third takes over as soon as one finishes, which shortened the
+            // LM head by 4% against a grid of exactly the resident
+            // workgroups. Not where a workgroup's start is dear: a late one
+            // pays the rmsnorm's float64 chain (or silu's exponentials) again
+            // on the critical path, and the argmax's last workgroup waits for
+            // every other one's atomics; those keep two.
+            const bool cheap_start = (xf == X_ENGINE || xf == X_Q8_0 || xf == X_F32) && argmax == nullptr;
+            waves = 4 > min_waves ? 4 : min_waves;
+            grid = (P.tiles + waves - 1) / waves;
+            const int cap = cus * (cheap_start ? 3 : 2);
+            if (grid > cap) grid = cap;
+        } else {
+            const int per_cu = (P.tiles + cus - 1) / cus;
+            waves = (per_cu + MID_TILES_PER_WAVE - 1) / MID_TILES_PER_WAVE;
+            if (waves < min_waves) waves = min_waves;
+            grid = (P.tiles + waves - 1) / waves;
+            if (grid > cus) grid = cus;
+        }
     }
     const int threads = 64 * waves;
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
