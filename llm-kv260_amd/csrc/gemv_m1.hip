@@ -220,10 +220,21 @@ __device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, X
     }
 }
 
+// The staged activation in LDS, one column per eight blocks (a chunk's
+// width): 64 dwords of int8 values (block j of the column at dword 8 j), the
+// eight fp32 scales, the eight int32 block sums, then 4 dwords of padding,
+// 84 dwords in all. Lane l of a wave reads column l % C, so the lanes of one
+// LDS pass read eight different columns: at a stride of 84 dwords their
+// 16-byte reads fall on distinct banks, where a stride of 64 sent all of them
+// to the same ones (8-way conflicts at K = 2048, 32-way at K = 8192).
+constexpr int XCOL_DWORDS = 84;
+constexpr int XCOL_D = 64;     // the scales' offset in a column
+constexpr int XCOL_S = 72;     // the block sums'
+__host__ __device__ constexpr size_t x_lds_bytes(int nb) { return (size_t)(nb / 8) * XCOL_DWORDS * 4; }
+
 // Quantize (if fp32) and store block b into LDS: int8 values, fp32 scale, int8 sum.
 template <int XF>
-__device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_q, float *s_d, int32_t *s_s,
-                                        float rms_scale = 0.0f) {
+__device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_x, float rms_scale = 0.0f) {
     uint32_t q[8];
     float dx;
     if constexpr (XF == X_ENGINE) {
@@ -279,11 +290,13 @@ __device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_q,
     int32_t sum = 0;
 #pragma unroll
     for (int m = 0; m < 8; ++m) sum = __builtin_amdgcn_sdot4((int)q[m], 0x01010101, sum, false);
-    u32x4 *dst = reinterpret_cast<u32x4 *>(s_q + 8 * b);
+    uint32_t *col = s_x + (b >> 3) * XCOL_DWORDS;
+    const int j = b & 7;
+    u32x4 *dst = reinterpret_cast<u32x4 *>(col + 8 * j);
     dst[0] = (u32x4){q[0], q[1], q[2], q[3]};
     dst[1] = (u32x4){q[4], q[5], q[6], q[7]};
-    s_d[b] = dx;
-    s_s[b] = sum;
+    col[XCOL_D + j] = __float_as_uint(dx);
+    col[XCOL_S + j] = (uint32_t)sum;
 }
 
 // The eight terms of one chunk.
@@ -348,9 +361,10 @@ __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// LDS layout (dynamic): per-wave slabs [waves][9216] | x int8[K] | x scale
-// f32[nb] | x sum i32[nb]. `block` / `nblocks` are this workgroup's index and
-// the number of workgroups sharing the matrix.
+// LDS layout (dynamic): per-wave slabs [waves][9216] | the staged activation
+// (nb / 8 columns of XCOL_DWORDS) | for X_RMS the float64 squares of x (33 per
+// block) and the scale. `block` / `nblocks` are this workgroup's index and the
+// number of workgroups sharing the matrix.
 // Raw buffer store of one fp32 to y[row]; a lane whose offset is past the end
 // of y stores nothing (the buffer unit drops out-of-range writes). Every lane
 // issues the instruction, so the number of memory operations a wave has in
@@ -405,9 +419,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     const int nthreads = blockDim.x;
     const int waves = nthreads >> 6;
     uint8_t *slab = lds + (size_t)wave * TILE_BYTES;
-    uint32_t *s_q = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
-    float *s_d = reinterpret_cast<float *>(s_q + 8 * nb);
-    int32_t *s_s = reinterpret_cast<int32_t *>(s_q + 9 * nb);
+    uint32_t *s_x = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
 
     const int C = P.C, rpw = P.rpw;
     const int my_r = lane / C;
@@ -450,18 +462,20 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         float rms = 0.0f;
         if constexpr (XF == X_RMS) {
             // rmsnorm's scale needs the whole of x: its squares go to LDS as
-            // float64 after the block sums, wave 0 reduces them, and the
-            // scale comes back through LDS.
-            double *sq = reinterpret_cast<double *>(s_s + nb);
-            float *s_rms = reinterpret_cast<float *>(sq + P.k);
+            // float64 after the staged x, wave 0 reduces them, and the scale
+            // comes back through LDS. Block b's 32 squares start at 33 b: the
+            // spare slot staggers the threads' 8-byte writes over the banks
+            // (at a stride of 32 they all hit the same two).
+            double *sq = reinterpret_cast<double *>(s_x + (nb / 8) * XCOL_DWORDS);
+            float *s_rms = reinterpret_cast<float *>(sq + P.k + P.k / 32);
             auto squares = [&](const XRaw<XF> &r, int b) {
 #pragma unroll
                 for (int m = 0; m < 8; ++m) {
                     const double a = r.v[m].x, c = r.v[m].y, d = r.v[m].z, e = r.v[m].w;
-                    sq[32 * b + 4 * m] = a * a;
-                    sq[32 * b + 4 * m + 1] = c * c;
-                    sq[32 * b + 4 * m + 2] = d * d;
-                    sq[32 * b + 4 * m + 3] = e * e;
+                    sq[33 * b + 4 * m] = a * a;
+                    sq[33 * b + 4 * m + 1] = c * c;
+                    sq[33 * b + 4 * m + 2] = d * d;
+                    sq[33 * b + 4 * m + 3] = e * e;
                 }
             };
             if (tid < nb) squares(xr, tid);
@@ -472,28 +486,28 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             }
             __syncthreads();
             if (wave == 0) {
-                const float sc = rms_scale_wave(sq, P.k, P.eps);
+                const float sc = rms_scale_wave<true>(sq, P.k, P.eps);
                 if (lane == 0) *s_rms = sc;
             }
             __syncthreads();
             rms = *s_rms;
         }
-        if (tid < nb) x_stage<XF>(xr, tid, s_q, s_d, s_s, rms);
+        if (tid < nb) x_stage<XF>(xr, tid, s_x, rms);
         for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
             XRaw<XF> xb;
             x_load<XF>(P.x, P.k, b, true, xb, P.norm_w);
-            x_stage<XF>(xb, b, s_q, s_d, s_s, rms);
+            x_stage<XF>(xb, b, s_x, rms);
         }
         __syncthreads();
-        const int cb = lane_live ? 8 * my_c : 0;
+        const uint32_t *col = s_x + (lane_live ? my_c : 0) * XCOL_DWORDS;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(s_q + 8 * (cb + j));
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(col + 8 * j);
             const u32x4 a = src[0], c = src[1];
             xv[j][0] = a.x; xv[j][1] = a.y; xv[j][2] = a.z; xv[j][3] = a.w;
             xv[j][4] = c.x; xv[j][5] = c.y; xv[j][6] = c.z; xv[j][7] = c.w;
-            xd[j] = s_d[cb + j];
-            xs[j] = s_s[cb + j];
+            xd[j] = __uint_as_float(col[XCOL_D + j]);
+            xs[j] = (int32_t)col[XCOL_S + j];
         }
     };
 
@@ -539,12 +553,32 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             float acc = 0.0f;
             if (r < rpw) {
                 const float *src = s_t + r * C * 9 + acc_a;
-                for (int c0 = 0; c0 < C; c0 += 8) {
+                if ((C & 7) == 0) {
+                    // Whole groups of eight (K a multiple of 2048): no guards,
+                    // and each group's reads go out before the previous
+                    // group's adds. The adds keep the chunk order.
                     float v[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = c0 + j < C ? src[9 * (c0 + j)] : 0.0f;
+                    for (int j = 0; j < 8; ++j) v[j] = src[9 * j];
+                    for (int c0 = 8; c0 < C; c0 += 8) {
+                        float nv[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) nv[j] = src[9 * (c0 + j)];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) acc = acc + v[j];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) v[j] = nv[j];
+                    }
 #pragma unroll
                     for (int j = 0; j < 8; ++j) acc = acc + v[j];
+                } else {
+                    for (int c0 = 0; c0 < C; c0 += 8) {
+                        float v[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) v[j] = c0 + j < C ? src[9 * (c0 + j)] : 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) acc = acc + v[j];
+                    }
                 }
             }
             return acc;
@@ -731,7 +765,7 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     // Staged activation: int8 values, fp32 scale and int32 sum per block; for
     // X_RMS also the squares of x as float64 and the rmsnorm scale.
     if (xf == X_RMS && w.k > 8192) return hipErrorInvalidValue;
-    const size_t x_lds = (size_t)nb * 40 + (xf == X_RMS ? (size_t)w.k * 8 + 16 : 0);
+    const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? (size_t)(w.k + w.k / 32) * 8 + 16 : 0);
     // Launch shape, from what bounds each size:
     //  * Small matrices (at most two tiles per CU): latency. One tile per
     //    wave, workgroups spread over every CU (each stages its own copy of
@@ -796,7 +830,7 @@ hipError_t launch_batch_pass(const BatchParams &B, int max_k, hipStream_t stream
     long blocks = 0;
     for (int i = 0; i < B.n; ++i) blocks += batch_blocks(B.e[i].rows, B.e[i].k, B.tiles_per_block);
     if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
-    const size_t lds = (size_t)(BATCH_THREADS / 64) * TILE_BYTES + (size_t)(max_k / QK) * 40;
+    const size_t lds = (size_t)(BATCH_THREADS / 64) * TILE_BYTES + x_lds_bytes(max_k / QK);
     static bool lds_allowed = false;
     if (!lds_allowed) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel<ONE_PASS>),

@@ -165,19 +165,23 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // the next B squares read while the current B are added; the result is
 // returned in every lane of the wave. The squares are written by the whole
 // workgroup beforehand, so the chains carry the adds and nothing else.
+// PAD: square i is stored at i + i / 32 (a spare slot after every 32), the
+// layout of a workgroup whose threads each write one 32-element block.
+template <bool PAD = false>
 __device__ __forceinline__ float rms_scale_wave(const double *sq, int n, float eps) {
     const int lane = threadIdx.x & 63;
+    auto at = [](int i) { return PAD ? i + (i >> 5) : i; };
     double acc = 0.0;
     if (lane < 4) {
         constexpr int B = 8;
         double cur[B], nxt[B];
 #pragma unroll
-        for (int t = 0; t < B; ++t) cur[t] = sq[lane + 4 * t];
+        for (int t = 0; t < B; ++t) cur[t] = sq[at(lane + 4 * t)];
         for (int base = 0; base < n; base += 4 * B) {
             // The last pass reads the first squares again (in range, unused).
             const int next = base + 4 * B < n ? base + 4 * B : 0;
 #pragma unroll
-            for (int t = 0; t < B; ++t) nxt[t] = sq[next + lane + 4 * t];
+            for (int t = 0; t < B; ++t) nxt[t] = sq[at(next + lane + 4 * t)];
 #pragma unroll
             for (int t = 0; t < B; ++t) acc = acc + cur[t];
 #pragma unroll
