@@ -18,13 +18,15 @@
 //    load order, ds_read_b128 in chunk order), so that lane l ends up with
 //    chunk l: 144 bytes, eight whole blocks.
 //  * Lane l owns chunk column c = l % C of the tile's rows. The tile is whole
-//    rows, so c never changes: the 256 int8 activations, 8 scales and 8 block
-//    sums of column c are read from LDS into registers once.
+//    rows, so c never changes: the 256 activations (as block_dot_nib takes
+//    them), 8 scales and 8 block corrections of column c are read from LDS
+//    into registers once.
 //  * The activation is staged once per workgroup in LDS (quantized there from
 //    fp32 by the fused entry points); its loads are issued before the first
 //    tiles', so they do not wait behind the weights.
-//  * Each block's dot is exact in int32: eight v_dot4_i32_i8 on the unsigned
-//    nibbles minus 8 * sum(x). Then t = (f32(sumi) * d_w) * d_x.
+//  * Each block's dot is exact in int32: twelve v_dot8_u32_u4 straight on the
+//    packed nibbles against the activation split into nibbles at staging
+//    (block_dot_nib). Then t = (f32(sumi) * d_w) * d_x.
 //  * The contract's order (src/llm_kv260/q4_0.py:170-182): lane a of a row
 //    adds the terms of blocks a, a + 8, a + 16, ... in that order, from +0.0f.
 //    Chunk c holds terms 8c .. 8c + 7, so accumulator a needs term a of every
@@ -221,18 +223,19 @@ __device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, X
 }
 
 // The staged activation in LDS, one column per eight blocks (a chunk's
-// width): 64 dwords of int8 values (block j of the column at dword 8 j), the
-// eight fp32 scales, the eight int32 block sums, then 4 dwords of padding,
-// 84 dwords in all. Lane l of a wave reads column l % C, so the lanes of one
+// width): 64 dwords of activation nibbles (x_nibbles of block j of the column
+// at dword 8 j), the eight fp32 scales, the eight int32 corrections
+// -8 * sum(x), then 4 dwords of padding, 84 dwords in all. Lane l of a wave reads column l % C, so the lanes of one
 // LDS pass read eight different columns: at a stride of 84 dwords their
 // 16-byte reads fall on distinct banks, where a stride of 64 sent all of them
 // to the same ones (8-way conflicts at K = 2048, 32-way at K = 8192).
 constexpr int XCOL_DWORDS = 84;
 constexpr int XCOL_D = 64;     // the scales' offset in a column
-constexpr int XCOL_S = 72;     // the block sums'
+constexpr int XCOL_S = 72;     // the corrections'
 __host__ __device__ constexpr size_t x_lds_bytes(int nb) { return (size_t)(nb / 8) * XCOL_DWORDS * 4; }
 
-// Quantize (if fp32) and store block b into LDS: int8 values, fp32 scale, int8 sum.
+// Quantize (if fp32) and store block b into LDS: its values as nibbles, its
+// fp32 scale, and -8 times the sum of its int8 values.
 template <int XF>
 __device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_x, float rms_scale = 0.0f) {
     uint32_t q[8];
@@ -290,13 +293,15 @@ __device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_x,
     int32_t sum = 0;
 #pragma unroll
     for (int m = 0; m < 8; ++m) sum = __builtin_amdgcn_sdot4((int)q[m], 0x01010101, sum, false);
+    uint32_t xn[8];
+    x_nibbles(q, xn);
     uint32_t *col = s_x + (b >> 3) * XCOL_DWORDS;
     const int j = b & 7;
     u32x4 *dst = reinterpret_cast<u32x4 *>(col + 8 * j);
-    dst[0] = (u32x4){q[0], q[1], q[2], q[3]};
-    dst[1] = (u32x4){q[4], q[5], q[6], q[7]};
+    dst[0] = (u32x4){xn[0], xn[1], xn[2], xn[3]};
+    dst[1] = (u32x4){xn[4], xn[5], xn[6], xn[7]};
     col[XCOL_D + j] = __float_as_uint(dx);
-    col[XCOL_S + j] = (uint32_t)sum;
+    col[XCOL_S + j] = (uint32_t)(-8 * sum);
 }
 
 // The eight terms of one chunk.
@@ -306,7 +311,7 @@ __device__ __forceinline__ void chunk_terms(const uint32_t w[CHUNK_DWORDS], cons
     {                                                                            \
         uint32_t d_bits, qs[4];                                                  \
         chunk_block<J>(w, d_bits, qs);                                           \
-        const int32_t sumi = block_dot_raw(qs, xv[J]) - 8 * xs[J];               \
+        const int32_t sumi = block_dot_nib(qs, xv[J], xs[J]);                    \
         t[J] = block_term(sumi, d_bits, xd[J]);                                  \
     }
     W4A8_TERM(0) W4A8_TERM(1) W4A8_TERM(2) W4A8_TERM(3)

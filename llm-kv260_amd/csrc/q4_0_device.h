@@ -42,20 +42,39 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
 }
 
 // Exact int32 dot of one Q4_0 block's 16 nibble bytes (four little-endian
-// dwords) with the block's 32 int8 activations (eight dwords). Byte j of the
-// block carries weight j in its low nibble and weight j + 16 in its high one
-// (q4_0.py:22-24). Nibbles 0..15 are non-negative int8 values, so v_dot4
-// gives sum(n * x) exactly and the -8 offset comes back as -8 * sum(x).
-__device__ __forceinline__ int32_t block_dot_raw(const uint32_t qs[4], const uint32_t xv[8]) {
-    int32_t acc = 0;
+// dwords) with the block's 32 int8 activations, on v_dot8_u32_u4 and no
+// unpacking. Byte j of the block carries weight j in its low nibble and
+// weight j + 16 in its high one (q4_0.py:22-24), so nibble 2e of dword k is
+// weight 4k + e and nibble 2e + 1 is weight 4k + e + 16. The activation comes
+// pre-split to match (x_nibbles): with x' = x + 128 (1..255, unsigned),
+// xn[k] holds the high nibbles of x'[4k + e] / x'[4k + e + 16] in nibbles
+// 2e / 2e + 1, and xn[4 + k] the low nibbles. Then, n being the unsigned
+// weight nibbles,
+//   sum((n - 8) x) = 16 sum(n a) + sum(n b) - 128 sum(n) - 8 sum(x)
+// with a, b the high and low nibbles of x'; every term is an exact unsigned
+// 4-bit dot, accumulated modulo 2^32, and c8 = -8 sum(x) seeds the b chain.
+// 12 dots and 2 integer ops per block, where splitting the nibbles for
+// v_dot4 took 21.
+__device__ __forceinline__ int32_t block_dot_nib(const uint32_t qs[4], const uint32_t xn[8], int32_t c8) {
+    uint32_t a = 0, b = (uint32_t)c8, n = 0;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const uint32_t lo = qs[m] & 0x0F0F0F0Fu;
-        const uint32_t hi = (qs[m] >> 4) & 0x0F0F0F0Fu;
-        acc = __builtin_amdgcn_sdot4((int)lo, (int)xv[m], acc, false);
-        acc = __builtin_amdgcn_sdot4((int)hi, (int)xv[4 + m], acc, false);
+    for (int k = 0; k < 4; ++k) {
+        a = __builtin_amdgcn_udot8(qs[k], xn[k], a, false);
+        b = __builtin_amdgcn_udot8(qs[k], xn[4 + k], b, false);
+        n = __builtin_amdgcn_udot8(qs[k], 0x11111111u, n, false);
     }
-    return acc;
+    return (int32_t)(16u * a + b) - 128 * (int32_t)n;
+}
+
+// The activation of one block as block_dot_nib takes it, from its eight
+// dwords of int8 values (byte e of q[m] is x[4m + e]).
+__device__ __forceinline__ void x_nibbles(const uint32_t q[8], uint32_t xn[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = q[k] ^ 0x80808080u, hi = q[4 + k] ^ 0x80808080u;   // x + 128, bytewise
+        xn[k] = ((lo >> 4) & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
+        xn[4 + k] = (lo & 0x0F0F0F0Fu) | ((hi << 4) & 0xF0F0F0F0u);
+    }
 }
 
 // The fp32 epilogue of one block, step 2 of the contract.
