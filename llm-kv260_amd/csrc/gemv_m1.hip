@@ -117,7 +117,7 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 constexpr int BATCH_THREADS = 64 * W4A8_BATCH_WAVES;
 constexpr int BATCH_TILES_PER_WAVE = W4A8_BATCH_TILES_PER_WAVE;
 #ifndef W4A8_MID_TILES_PER_WAVE
-#define W4A8_MID_TILES_PER_WAVE 4
+#define W4A8_MID_TILES_PER_WAVE 1
 #endif
 constexpr int MID_TILES_PER_WAVE = W4A8_MID_TILES_PER_WAVE;
 
@@ -776,10 +776,10 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     //    wave, workgroups spread over every CU (each stages its own copy of
     //    x in parallel).
     //  * Mid-size (up to eight tiles per CU): one workgroup per CU whose waves
-    //    walk up to MID_TILES_PER_WAVE tiles each, so a wave computes one
-    //    tile while the next is still arriving (four per wave rather than one
-    //    took gate|up from 7.2 to 6.7 us; down, at four tiles per CU, keeps
-    //    one per wave for its activation's 256 blocks).
+    //    walk MID_TILES_PER_WAVE tiles each. One per wave, every tile in
+    //    flight at once: gate|up 5.8 us, against 6.0 at four per wave and
+    //    6.4 at two. (Before the staged activation was padded against bank
+    //    conflicts, four per wave had been the faster.)
     //  * Large: bandwidth. Four-wave workgroups, every wave walking tiles
     //    with a stride of the whole grid, at most eight resident waves per CU
     //    (two tiles and the activation column take about 208 VGPRs, two
