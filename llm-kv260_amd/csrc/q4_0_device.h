@@ -106,10 +106,14 @@ __device__ __forceinline__ void chunk_block(const uint32_t w[CHUNK_DWORDS], uint
 // Q8_0 quantization of one 32-element block, q4_0.py:83-97:
 // amax = max|x|, d = amax / 127, inv = d == 0 ? 0 : 1 / d (both correctly
 // rounded fp32 divisions), q = sign(s) * floor(|s| + 0.5) with s = x * inv.
+// The sign goes on before the conversion: |s| + 0.5 is computed (and
+// rounded) exactly as the contract writes it, copysign moves s's sign onto
+// it, and the conversion truncates toward zero, which is floor for the
+// magnitude in both signs. So the result is sign(s) * floor(|s| + 0.5) with
+// no compare (-0 and NaN give 0, as the compare-and-negate form does).
 __device__ __forceinline__ int8_t q8_round(float x, float inv) {
     const float s = x * inv;
-    const float mag = floorf(fabsf(s) + 0.5f);
-    return (int8_t)(int)(s < 0.0f ? -mag : mag);
+    return (int8_t)(int)copysignf(fabsf(s) + 0.5f, s);
 }
 
 __device__ __forceinline__ float q8_scale(float amax) { return amax / 127.0f; }
