@@ -3,9 +3,12 @@
 // src/llm_kv260/q4_0.py:83-97) and a Q4_0 weight quantizer
 // (src/llm_kv260/q4_0.py:100-121) for building matrices on the device.
 //
-// Both are element-wise over 32-element blocks: one thread per block, 32
-// floats in through eight 16-byte loads. They are tiny next to the GEMV
-// (K floats per activation; weights are quantized once).
+// Both are element-wise over 32-element blocks. The activation quantizers
+// give each block eight threads (one 16-byte load, four values each) and
+// meet for the block's max through DPP: a launch of them is latency, and a
+// thread that quantized a whole block alone spent ~250 instructions on it.
+// The weight quantizer keeps one thread per block (weights are quantized
+// once).
 #include "kernels.h"
 #include "q4_0_device.h"
 
@@ -58,16 +61,46 @@ __device__ __forceinline__ void quantize_store(const float v[32], int row, int b
     }
 }
 
+// Q8_0 of values 4g .. 4g + 3 of a 32-element block, thread g (0..7) of an
+// aligned group of eight: amax is the group's max (DPP quad_perm [1,0,3,2],
+// [2,3,0,1], then row_half_mirror), so every thread computes the same d and
+// inv as a thread holding the whole block, and its four bytes are the ones
+// quantize_store would write there.
+template <int OUT>
+__device__ __forceinline__ void quantize_store8(const float4 v, int row, int b, int g, int k, uint8_t *__restrict__ out) {
+    const int nb = k >> 5;
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, dpp_mov<0xB1>(amax));
+    amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+    amax = fmaxf(amax, dpp_mov<0x141>(amax));
+    const float d = q8_scale(amax);
+    const float inv = safe_recip(d);
+    const uint32_t word = (uint32_t)(uint8_t)q8_round(v.x, inv) | ((uint32_t)(uint8_t)q8_round(v.y, inv) << 8) |
+                          ((uint32_t)(uint8_t)q8_round(v.z, inv) << 16) | ((uint32_t)(uint8_t)q8_round(v.w, inv) << 24);
+    const uint16_t dh = float_to_half_bits(d);
+    if constexpr (OUT == X_ENGINE) {
+        uint8_t *rowp = out + (size_t)row * (k + 4 * nb);
+        reinterpret_cast<uint32_t *>(rowp + 32 * b)[g] = word;
+        if (g == 0) reinterpret_cast<float *>(rowp + k)[b] = half_bits_to_float(dh);
+    } else {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(out + ((size_t)row * nb + b) * Q8_0_BYTES);
+        if (g == 0) dst[0] = dh;
+        dst[1 + 2 * g] = (uint16_t)(word & 0xFFFFu);
+        dst[2 + 2 * g] = (uint16_t)(word >> 16);
+    }
+}
+
 template <int OUT>
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int k, int m,
                                                             uint8_t *__restrict__ out) {
     const int nb = k >> 5;
     const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (long)nb * m) return;
-    const int row = (int)(gid / nb), b = (int)(gid - (long)row * nb);
-    float v[32];
-    load_block(x + (size_t)row * k + 32 * b, v);
-    quantize_store<OUT>(v, row, b, k, out);
+    if (gid >= (long)nb * m * 8) return;           // whole groups of eight leave together
+    const long blk = gid >> 3;
+    const int g = (int)(gid & 7);
+    const int row = (int)(blk / nb), b = (int)(blk - (long)row * nb);
+    const float4 v = reinterpret_cast<const float4 *>(x + (size_t)row * k + 32 * b)[g];
+    quantize_store8<OUT>(v, row, b, g, k, out);
 }
 
 // act = silu(gate) * up (tp_llama.cpp:612-619) of m rows gate | up
@@ -76,14 +109,15 @@ __global__ __launch_bounds__(256) void silu_mul_q8_0_kernel(const float *__restr
                                                             uint8_t *__restrict__ out) {
     const int nb = k >> 5;
     const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (long)nb * m) return;
-    const int row = (int)(gid / nb), b = (int)(gid - (long)row * nb);
-    float g[32], u[32], v[32];
-    load_block(gate_up + (size_t)row * 2 * k + 32 * b, g);
-    load_block(gate_up + (size_t)row * 2 * k + k + 32 * b, u);
-#pragma unroll
-    for (int e = 0; e < 32; ++e) v[e] = silu_mul(g[e], u[e]);
-    quantize_store<X_ENGINE>(v, row, b, k, out);
+    if (gid >= (long)nb * m * 8) return;           // whole groups of eight leave together
+    const long blk = gid >> 3;
+    const int t = (int)(gid & 7);
+    const int row = (int)(blk / nb), b = (int)(blk - (long)row * nb);
+    const float *src = gate_up + (size_t)row * 2 * k + 32 * b;
+    const float4 g = reinterpret_cast<const float4 *>(src)[t];
+    const float4 u = reinterpret_cast<const float4 *>(src + k)[t];
+    const float4 v = make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
+    quantize_store8<X_ENGINE>(v, row, b, t, k, out);
 }
 
 // h = rmsnorm(x) * norm_w (tp_llama.cpp:557-569) of m rows of float32[k],
@@ -163,11 +197,12 @@ __global__ __launch_bounds__(256) void quantize_q4_0_kernel(const float *__restr
 hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFormat out_fmt, hipStream_t stream) {
     const long blocks = (long)(k / 32) * m;
     if (blocks == 0) return hipSuccess;
-    const int grid = (int)((blocks + 255) / 256);
+    const long grid = (8 * blocks + 255) / 256;
+    if (grid > 0x7fffffffL) return hipErrorInvalidValue;
     if (out_fmt == X_ENGINE)
-        hipLaunchKernelGGL(quantize_q8_0_kernel<X_ENGINE>, dim3(grid), dim3(256), 0, stream, x, k, m, out);
+        hipLaunchKernelGGL(quantize_q8_0_kernel<X_ENGINE>, dim3((unsigned)grid), dim3(256), 0, stream, x, k, m, out);
     else if (out_fmt == X_Q8_0)
-        hipLaunchKernelGGL(quantize_q8_0_kernel<X_Q8_0>, dim3(grid), dim3(256), 0, stream, x, k, m, out);
+        hipLaunchKernelGGL(quantize_q8_0_kernel<X_Q8_0>, dim3((unsigned)grid), dim3(256), 0, stream, x, k, m, out);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -176,7 +211,7 @@ hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFor
 hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out, hipStream_t stream) {
     const long blocks = (long)(k / 32) * m;
     if (blocks == 0) return hipSuccess;
-    const long grid = (blocks + 255) / 256;
+    const long grid = (8 * blocks + 255) / 256;
     if (grid > 0x7fffffffL) return hipErrorInvalidValue;
     hipLaunchKernelGGL(silu_mul_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, stream, gate_up, k, m, out);
     return hipGetLastError();
