@@ -21,6 +21,12 @@ Prints one JSON line. Besides the chain (value), it reports:
   gemv         microseconds per GEMV at every shape, weights rotated past the
                Infinity Cache, launched back to back from a HIP graph
   gemm         the M > 1 sweep (M = 1 .. 64) at gate|up and down
+  lm_head_argmax  the LM head with its greedy pick fused, and the sampler's
+               top-40 candidates of the same logits (w4a8_topk)
+  producers    rmsnorm / silu*up fused into the GEMV's staging against the
+               standalone producer then the GEMV
+  chain_fused_producers  the chain with those producers and the argmax
+  prefill      24- and 64-token prompts through the 65 matrices (M > 1 GEMM)
   caller       the reference's decode-side caller (engine_t of
                board/tp/tp_llama.cpp, rebuilt against the reference driver
                headers: llm-kv260_amd/caller/engine_caller) on both engines:
@@ -169,9 +175,20 @@ def time_lm_argmax(torch, kv, cf, stream):
     g = graph_of(torch, stream, calls)
     ms, _ = time_replays(torch, stream, g, 10, 2)
     us = ms * 1e3 / launches
+    del g
+    # The sampler's candidates over the same logits (w4a8_topk, two launches).
+    k = 40
+    vals = torch.empty(k, dtype=torch.float32, device="cuda")
+    idx = torch.empty(k, dtype=torch.int32, device="cuda")
+    tws = torch.empty(L.w4a8_topk_workspace_bytes(m.rows), dtype=torch.uint8, device="cuda")
+    g = graph_of(torch, stream, [lambda s: kv.check("w4a8_topk", L.w4a8_topk(
+        y.data_ptr(), m.rows, k, vals.data_ptr(), idx.data_ptr(), tws.data_ptr(), tws.numel(), s))] * launches)
+    ms_k, _ = time_replays(torch, stream, g, 10, 2)
     del g, mats, base
     return {"shape": f"{m.rows}x{m.k}", "us": round(us, 3), "gbps": round(m.algorithmic_bytes / us / 1e3, 1),
-            "argmax": int(best.cpu()[0]), "weight_copies": 3}
+            "argmax": int(best.cpu()[0]), "weight_copies": 3,
+            "topk": {"k": k, "us": round(ms_k * 1e3 / launches, 3), "first": int(idx.cpu()[0]),
+                     "launches": 2}}
 
 
 def time_producers(torch, kv, cf, stream):
@@ -443,6 +460,8 @@ def main() -> int:
         log(f"producer {name} {r['shape']}: fused {r['fused_us']} us, two launches {r['two_launches_us']} us")
     lm_argmax = time_lm_argmax(torch, kv, cf, stream)
     log(f"gemv lm_head + argmax: {lm_argmax['us']} us, {lm_argmax['gbps']} GB/s")
+    log(f"top-{lm_argmax['topk']['k']} candidates of the logits: {lm_argmax['topk']['us']} us "
+        f"(first {lm_argmax['topk']['first']}, argmax {lm_argmax['argmax']})")
     lm = gemv["lm_head"]
     lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 

@@ -83,6 +83,19 @@ size_t w4a8_argmax_workspace_bytes(void);
 int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int k, int32_t *argmax,
                          void *workspace, size_t workspace_bytes, void *stream);
 
+/* The sampler's candidates (board/tp/tp_llama.cpp:894-909): the k best
+ * logits of y[0..n), 1 <= k <= 64, as vals[k] / idx[k] in the order the
+ * reference's insertion sort leaves them: values descending, among equal
+ * values (-0 equal to +0) the smaller index first, and a value at or below
+ * -1e30 never admitted; slots left over hold {-1e30, 0} as there. vals are
+ * y's own values (bit for bit). A NaN logit is never a candidate (the
+ * reference's handling of one depends on its position). Two launches
+ * through `workspace`: w4a8_topk_workspace_bytes(n) bytes of device memory,
+ * 8-byte aligned, overwritten by each call. 1 <= n <= 262144. */
+size_t w4a8_topk_workspace_bytes(int n);
+int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *workspace, size_t workspace_bytes,
+              void *stream);
+
 /* The reference's producers of the GEMV input, fused into the GEMV's own
  * activation staging (board/tp/tp_llama.cpp, computed as it does):
  *   rmsnorm (:557-569): h = x * (1 / sqrtf((float)(ss / k) + eps)) * norm_w,

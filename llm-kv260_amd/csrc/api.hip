@@ -92,6 +92,17 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
     return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream, argmax, workspace));
 }
 
+size_t w4a8_topk_workspace_bytes(int n) { return topk_workspace_bytes(n); }
+
+int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *workspace, size_t workspace_bytes,
+              void *stream) {
+    if (!y || !vals || !idx || !workspace) return W4A8_ERR_NULL;
+    if (n < 1 || n > topk_max_n() || k < 1 || k > 64) return W4A8_ERR_SHAPE;
+    if (!aligned(y, 4) || !aligned(vals, 4) || !aligned(idx, 4) || !aligned(workspace, 8)) return W4A8_ERR_ALIGN;
+    if (workspace_bytes < topk_workspace_bytes(n)) return W4A8_ERR_SHAPE;
+    return hip_status(launch_topk(y, n, k, vals, idx, workspace, (hipStream_t)stream));
+}
+
 // The fused rmsnorm stages x's float64 squares in LDS: k <= 8192.
 constexpr int RMS_FUSED_MAX_K = 8192;
 

@@ -51,6 +51,15 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
                           int32_t *argmax = nullptr, void *workspace = nullptr, XAux aux = XAux{});
 size_t argmax_workspace_bytes();   // of the current device
 
+// The k (1..64) best of y[0..n) as the reference's sampler selects them
+// (values descending, the smaller index first among equals, never a value at
+// or below -1e30): two launches, the candidate lists of 1024-logit slices in
+// `workspace` (topk_workspace_bytes(n)). n <= topk_max_n().
+hipError_t launch_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *workspace,
+                       hipStream_t stream);
+size_t topk_workspace_bytes(int n);
+int topk_max_n();
+
 // y[m][rows] for m activation rows in engine layout (row stride K + K/8 bytes).
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, float *y, hipStream_t stream);
 

@@ -39,7 +39,7 @@ EXPORTS = (
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
     "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
     "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
-    "w4a8_silu_mul_q8_0",
+    "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -114,6 +114,10 @@ def lib() -> ctypes.CDLL:
     L.w4a8_rmsnorm_q8_0.restype = i
     L.w4a8_silu_mul_q8_0.argtypes = [p, p, i, i, p]
     L.w4a8_silu_mul_q8_0.restype = i
+    L.w4a8_topk_workspace_bytes.argtypes = [i]
+    L.w4a8_topk_workspace_bytes.restype = ctypes.c_size_t
+    L.w4a8_topk.argtypes = [p, i, i, p, p, p, ctypes.c_size_t, p]
+    L.w4a8_topk.restype = i
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
         getattr(L, f).argtypes = [p, i, p]
         getattr(L, f).restype = i
@@ -285,6 +289,25 @@ def argmax_workspace():
     """A zero-filled workspace for gemv_q4_0_f32_argmax on the current device."""
     import torch
     return torch.zeros(lib().w4a8_argmax_workspace_bytes(), dtype=torch.uint8, device="cuda")
+
+
+def topk(y, k: int, workspace=None):
+    """The sampler's k candidates of the logits y (board/tp/tp_llama.cpp:894-909):
+    (vals float32 [k], idx int32 [k]) on the GPU, values descending, the smaller
+    index first among equals, never a value at or below -1e30 (left-over slots
+    hold -1e30 and index 0). 1 <= k <= 64."""
+    import torch
+    _need(y, torch.float32, "y")
+    if y.dim() != 1:
+        raise ValueError(f"y must be 1-D, got {tuple(y.shape)}")
+    n = y.shape[0]
+    if workspace is None:
+        workspace = torch.empty(max(lib().w4a8_topk_workspace_bytes(n), 8), dtype=torch.uint8, device=y.device)
+    vals = torch.empty(k, dtype=torch.float32, device=y.device)
+    idx = torch.empty(k, dtype=torch.int32, device=y.device)
+    check("w4a8_topk", lib().w4a8_topk(y.data_ptr(), n, k, vals.data_ptr(), idx.data_ptr(), workspace.data_ptr(),
+                                       workspace.numel() * workspace.element_size(), _stream(y)))
+    return vals, idx
 
 
 def gemv_q4_0_f32_argmax(blocks, k: int, x, workspace, out=None):

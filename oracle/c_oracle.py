@@ -49,6 +49,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_ggml_expf.argtypes = [ctypes.c_float]
         L.oracle_ggml_expf.restype = ctypes.c_float
         L.oracle_silu_mul.argtypes = [p, p, i64, p]
+        L.oracle_topk.argtypes = [p, i64, ctypes.c_int, p, p]
         _lib = L
     return _lib
 
@@ -152,3 +153,13 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     out = np.empty_like(g)
     lib().oracle_silu_mul(g.ctypes.data, u.ctypes.data, g.size, out.ctypes.data)
     return out
+
+
+def topk(y: np.ndarray, k: int):
+    """board/tp/tp_llama.cpp:894-909's candidate selection on float32 [n]:
+    (vals float32 [k], idx int32 [k])."""
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    vals = np.empty(k, dtype=np.float32)
+    idx = np.empty(k, dtype=np.int32)
+    lib().oracle_topk(y.ctypes.data, y.size, int(k), vals.ctypes.data, idx.ctypes.data)
+    return vals, idx

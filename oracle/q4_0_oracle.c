@@ -252,4 +252,28 @@ void oracle_silu_mul(const float *g, const float *u, int64_t n, float *out) {
     }
 }
 
+/* The sampler's per-shard candidates, tp_llama.cpp:894-909, restated: k
+ * slots start as {-1e30, 0}; each y[i] in increasing i is skipped when
+ * y[i] <= the last slot's value, else inserted after every held value that is
+ * not less than it (the shift loop stops at an equal value), the last slot
+ * falling out. The reference's loop exactly, NaN included. */
+void oracle_topk(const float *y, int64_t n, int k, float *vals, int32_t *idx) {
+    for (int j = 0; j < k; ++j) {
+        vals[j] = -1e30f;
+        idx[j] = 0;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = y[i];
+        if (v <= vals[k - 1]) continue;
+        int pos = k - 1;
+        while (pos > 0 && vals[pos - 1] < v) {
+            vals[pos] = vals[pos - 1];
+            idx[pos] = idx[pos - 1];
+            --pos;
+        }
+        vals[pos] = v;
+        idx[pos] = (int32_t)i;
+    }
+}
+
 const char *oracle_contract_version(void) { return "llm-kv260/w4a8-q4_0-v2"; }
