@@ -241,13 +241,16 @@ def time_producers(torch, kv, cf, stream):
     return out
 
 
-def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup):
+def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu_epilogue=True):
     """The decode step with its producers fused and its one in-step data
     dependency kept: per layer q|k|v = W rmsnorm(x), o = W x, gate|up =
     W rmsnorm(x), down = W (silu(gate) * up) of gate|up's own output; the LM
     head = W rmsnorm(x) with its greedy pick. The rmsnorm inputs (the residual
     stream) and o's input (the attention output) are seeded vectors: attention
-    and the residual adds are not part of the engine."""
+    and the residual adds are not part of the engine. silu_epilogue: gate|up
+    computes silu(gate) * up as its epilogue (w4a8_gemv_gate_up_silu) and down
+    quantizes that; otherwise down computes silu in its own staging
+    (w4a8_gemv_silu_mul)."""
     L = kv.lib()
     g = torch.Generator(device="cuda")
     g.manual_seed(6)
@@ -261,7 +264,14 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup):
     for i, m in enumerate(chain):
         w, y = mats[i], ys[i]
         role = "lm" if i == len(chain) - 1 else ("qkv", "o", "gate_up", "down")[i % 4]
-        if role in ("qkv", "gate_up"):
+        if role == "gate_up" and silu_epilogue:
+            calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_gate_up_silu(
+                w.data_ptr(), resid.data_ptr(), norm.data_ptr(), 1e-5, y.data_ptr(), m.rows, m.k, s))(w, y, m))
+        elif role == "down" and silu_epilogue:
+            act = ys[i - 1]                                  # gate|up's act, its first half
+            calls.append((lambda w, y, m, act: lambda s: L.w4a8_gemv_f32(w.data_ptr(), act.data_ptr(), y.data_ptr(),
+                                                                         m.rows, m.k, s))(w, y, m, act))
+        elif role in ("qkv", "gate_up"):
             calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_rmsnorm(w.data_ptr(), resid.data_ptr(), norm.data_ptr(),
                                                                         1e-5, y.data_ptr(), m.rows, m.k, s))(w, y, m))
         elif role == "o":
@@ -281,6 +291,7 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup):
     del gr
     return {"us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "launches_per_step": len(calls),
             "gbps": round(cf.chain_algorithmic_bytes() / (ms * 1e-3) / 1e9, 1),
+            "silu": "gate|up epilogue" if silu_epilogue else "down's staging",
             "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
 
 
@@ -438,8 +449,11 @@ def main() -> int:
         log(f"prefill {r['tokens']} tokens: {r['ms_per_prompt']} ms, {r['tokens_per_s']} tokens/s "
             f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token)")
     fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup)
+    staged = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, silu_epilogue=False)
+    fused_chain["silu_in_down_staging_us_per_step"] = staged["us_per_step"]
     log(f"fused chain: {fused_chain['us_per_step']} us/step, {fused_chain['tokens_per_s']} tokens/s "
-        "(rmsnorm / silu fused, LM head with argmax)")
+        f"(rmsnorm fused, silu in gate|up's epilogue, LM head with argmax); {staged['us_per_step']} us/step "
+        "with silu in down's staging")
 
     gemv, gemm = {}, []
     shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES

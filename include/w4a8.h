@@ -116,6 +116,17 @@ int w4a8_gemv_rmsnorm_argmax(const void *w, const float *x, const float *norm_w,
                              int32_t *argmax, void *workspace, size_t workspace_bytes, void *stream);
 int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, int k, void *stream);
 
+/* The gate|up GEMV with silu as its epilogue: y = W Q8_0(h) over rows = 2n
+ * (gate rows, then up rows, as the reference fuses them, tp_llama.cpp:258-268)
+ * with h = rmsnorm(x) * norm_w as w4a8_gemv_rmsnorm (norm_w != NULL) or
+ * h = x (norm_w NULL), and act[i] = silu(y[i]) * y[n + i] (tp_llama.cpp:612-
+ * 619, ggml's vector expf) written in place of y: float32[n], the activation
+ * of down. Byte-identical to that GEMV followed by silu_mul, with silu
+ * computed once per output instead of by every workgroup of down.
+ * 2048 <= k <= 8192, n a multiple of 64 / (k / 256). */
+int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, float eps, float *act, int rows, int k,
+                           void *stream);
+
 /* The same producers on their own, m rows, quantized to the engine layout
  * (row stride w4a8_engine_x_bytes(k)): the input of w4a8_gemv / w4a8_gemm. */
 int w4a8_rmsnorm_q8_0(const float *x, const float *norm_w, float eps, void *out_engine, int k, int m, void *stream);

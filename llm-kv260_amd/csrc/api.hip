@@ -92,6 +92,18 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
     return hip_status(launch_gemv_m1(plain_matrix(w, rows, k), x, X_F32, y, (hipStream_t)stream, argmax, workspace));
 }
 
+int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, float eps, float *act, int rows,
+                           int k, void *stream) {
+    if (int s = check_gemv(w, x, act, rows, k, 16)) return s;
+    if (k < 2048 || k > 8192 || rows % 2 || (rows / 2) % (64 / (k / 256))) return W4A8_ERR_SHAPE;
+    if (norm_w && !aligned(norm_w, 16)) return W4A8_ERR_ALIGN;
+    XAux aux;
+    aux.norm_w = norm_w;
+    aux.eps = eps;
+    return hip_status(launch_gemv_gate_up_silu(static_cast<const uint8_t *>(w), x, norm_w ? X_RMS : X_F32, act, rows,
+                                               k, (hipStream_t)stream, aux));
+}
+
 size_t w4a8_topk_workspace_bytes(int n) { return topk_workspace_bytes(n); }
 
 int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *workspace, size_t workspace_bytes,

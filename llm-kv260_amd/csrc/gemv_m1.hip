@@ -415,7 +415,12 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
     }
 }
 
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false>
+// PAIR: the gate|up GEMV with silu(gate) * up as its epilogue. A wave's two
+// tiles are t and t + tiles / 2 (the grid has exactly tiles / 2 waves):
+// rows r and r + rows / 2, gate and up of the same output. The gate's y stays
+// in the lane's register until the up tile's y is ready, and only
+// act[r] = silu_mul(gate, up) is stored, to y[0 .. rows / 2).
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false>
 __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
@@ -518,7 +523,9 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
 
     const int acc_r = lane >> 3, acc_a = lane & 7;
     unsigned long long best = 0;          // argmax epilogue: this lane's best key
-    const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * P.rows, BUFFER_DWORD3);
+    const __amdgpu_buffer_rsrc_t y_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * (PAIR ? P.rows / 2 : P.rows), BUFFER_DWORD3);
+    float held = 0.0f;                    // PAIR: this lane's gate value
     // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
     // slab -> ordered lane sums -> tree -> y; with REFILL the buffer then
     // receives the tile DEPTH strides ahead while the terms are computed.
@@ -588,7 +595,16 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             }
             return acc;
         };
-        if constexpr (ONE_PASS) {
+        if constexpr (PAIR) {
+            // Both halves issue one store; the gate's goes out of range.
+            const float yv = tree8_dpp(lane_sum(acc_r));
+            const int row = tile * rpw + acc_r;
+            const bool up = tile >= (P.tiles >> 1);
+            const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
+            held = up ? held : yv;
+            const float act = silu_mul(held, yv);
+            store_y(y_rsrc, up && mine ? 4 * (row - (P.rows >> 1)) : OUT_OF_RANGE, act);
+        } else if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
             const int row = tile * rpw + acc_r;
             const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
@@ -642,10 +658,10 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     if constexpr (ARGMAX) argmax_finish(P, best, nblocks, lds);
 }
 
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false>
 __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX>(P, blockIdx.x, gridDim.x, lds);
+    gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>(P, blockIdx.x, gridDim.x, lds);
 }
 
 __host__ __device__ inline void derive_plain(GemvParams &P, const uint8_t *w, const void *x, float *y, int rows, int k) {
@@ -694,11 +710,11 @@ __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2
     gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, lds);
 }
 
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX, bool PAIR = false>
 hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
     // Dynamic LDS above the default 64 KB must be allowed per kernel once.
     static bool lds_allowed = false;
-    const void *fn = reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX>);
+    const void *fn = reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>);
     if (!lds_allowed) {
         // What the kernel's static LDS (the argmax flag) leaves of the budget.
         hipFuncAttributes attr{};
@@ -709,7 +725,7 @@ hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, h
         if (e != hipSuccess) return e;
         lds_allowed = true;
     }
-    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX>), dim3(grid), dim3(threads), lds, stream, P);
+    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), dim3(grid), dim3(threads), lds, stream, P);
     return hipGetLastError();
 }
 
@@ -845,6 +861,33 @@ hipError_t launch_batch_pass(const BatchParams &B, int max_k, hipStream_t stream
     }
     hipLaunchKernelGGL(gemv_batch_kernel<ONE_PASS>, dim3((unsigned)blocks), dim3(BATCH_THREADS), lds, stream, B);
     return hipGetLastError();
+}
+
+hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, float *act, int rows, int k,
+                                    hipStream_t stream, XAux aux) {
+    if ((xf != X_F32 && xf != X_RMS) || k % 256 || k < 2048 || k > 8192 || rows < 2 || rows % 2) return hipErrorInvalidValue;
+    GemvParams P{};
+    derive_plain(P, w, x, act, rows, k);
+    P.norm_w = aux.norm_w;
+    P.eps = aux.eps;
+    // Tiles may not straddle the two halves.
+    if ((rows / 2) % P.rpw) return hipErrorInvalidValue;
+    const int half = P.tiles / 2;
+    const int nb = k / QK;
+    const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;
+    // The grid has exactly `half` waves, so that a wave's second tile is its first + half.
+    int waves = 0;
+    for (int wv = 4; wv >= min_waves && wv >= 1; wv >>= 1)
+        if (half % wv == 0) {
+            waves = wv;
+            break;
+        }
+    if (waves == 0) return hipErrorInvalidValue;
+    const int grid = half / waves;
+    const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? (size_t)(k + k / 32) * 8 + 16 : 0);
+    const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
+    if (xf == X_RMS) return launch_pass<X_RMS, true, true, false, true>(P, grid, 64 * waves, lds, stream);
+    return launch_pass<X_F32, true, true, false, true>(P, grid, 64 * waves, lds, stream);
 }
 
 hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream) {

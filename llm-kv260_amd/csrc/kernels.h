@@ -83,6 +83,10 @@ hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream)
 
 // The same GEMVs with no order between them, in one launch.
 hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream);
+// gate|up (rows = 2 n) with silu(gate) * up as the epilogue: act[n] from
+// x as X_F32 or X_RMS (aux), 2048 <= k <= 8192, n a multiple of 64 / (k / 256).
+hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, float *act, int rows, int k,
+                                    hipStream_t stream, XAux aux = XAux{});
 
 // w: float32[rows][K] -> Q4_0 rows.
 hipError_t launch_quantize_q4_0(const float *w, int rows, int k, uint8_t *out, hipStream_t stream);

@@ -39,7 +39,7 @@ EXPORTS = (
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
     "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
     "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
-    "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk",
+    "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk", "w4a8_gemv_gate_up_silu",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -118,6 +118,8 @@ def lib() -> ctypes.CDLL:
     L.w4a8_topk_workspace_bytes.restype = ctypes.c_size_t
     L.w4a8_topk.argtypes = [p, i, i, p, p, p, ctypes.c_size_t, p]
     L.w4a8_topk.restype = i
+    L.w4a8_gemv_gate_up_silu.argtypes = [p, p, p, f32, p, i, i, p]
+    L.w4a8_gemv_gate_up_silu.restype = i
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
         getattr(L, f).argtypes = [p, i, p]
         getattr(L, f).restype = i
@@ -289,6 +291,25 @@ def argmax_workspace():
     """A zero-filled workspace for gemv_q4_0_f32_argmax on the current device."""
     import torch
     return torch.zeros(lib().w4a8_argmax_workspace_bytes(), dtype=torch.uint8, device="cuda")
+
+
+def gemv_gate_up_silu(blocks, k: int, x, norm_w=None, eps: float = 1e-5, out=None):
+    """act = silu(gate) * up of the gate|up GEMV y = W Q8_0(rmsnorm(x) * norm_w)
+    (or of x itself when norm_w is None), rows = 2n gate rows then up rows:
+    float32 [n], in one kernel (board/tp/tp_llama.cpp:557-569, 612-619)."""
+    import torch
+    _need(x, torch.float32, "x")
+    _check_blocks(blocks, k)
+    if tuple(x.shape) != (k,):
+        raise ValueError(f"x must be [{k}], got {tuple(x.shape)}")
+    rows = blocks.shape[0]
+    act = torch.empty(rows // 2, dtype=torch.float32, device=blocks.device) if out is None else out
+    if norm_w is not None:
+        _need(norm_w, torch.float32, "norm_w")
+    check("w4a8_gemv_gate_up_silu", lib().w4a8_gemv_gate_up_silu(
+        blocks.data_ptr(), x.data_ptr(), None if norm_w is None else norm_w.data_ptr(), float(eps), act.data_ptr(),
+        rows, k, _stream(blocks)))
+    return act
 
 
 def topk(y, k: int, workspace=None):

@@ -106,3 +106,36 @@ def test_lm_head_step(gpu):
         y, best = gpu.gemv_rmsnorm_argmax(dev(blocks), k, dev(x), dev(w), 1e-5, ws)
         assert_bytes_equal(host(y), want, "lm head step")
         assert int(host(best)[0]) == scan_argmax(want)
+
+
+@pytest.mark.parametrize("rows,k,rms", [(16384, 2048, True), (16384, 2048, False), (256, 8192, True),
+                                        (4096, 4096, False), (16, 2048, True)])
+def test_gemv_gate_up_silu(gpu, rows, k, rms):
+    """gate|up with silu(gate) * up as the epilogue: act = silu_mul(y[:n], y[n:])
+    of the plain (or rmsnorm-fed) GEMV, byte for byte."""
+    print(f"gate_up_silu rows={rows} k={k} rms={rms}", flush=True)
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 90 + rows, 0.02))
+    rng = np.random.default_rng(rows + k)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    w = rng.standard_normal(k).astype(np.float32) if rms else None
+    h = C.rmsnorm(x, w, 1e-5) if rms else x
+    xq, xd = C.quantize_q8_0(h)
+    y = C.gemv_q4_0(blocks, k, xq, xd)
+    n = rows // 2
+    want = C.silu_mul(y[:n], y[n:])
+    got = gpu.gemv_gate_up_silu(dev(blocks), k, dev(x), None if w is None else dev(w), 1e-5)
+    assert_bytes_equal(host(got), want, f"gate_up_silu {rows}x{k}")
+
+
+def test_gemv_gate_up_silu_rejects(gpu):
+    import torch
+    L = gpu.lib()
+    w = torch.zeros(64 * 2048 // 32 * 18, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(2048, dtype=torch.float32, device="cuda")
+    act = torch.zeros(64, dtype=torch.float32, device="cuda")
+    call = lambda rows, k: L.w4a8_gemv_gate_up_silu(w.data_ptr(), x.data_ptr(), None, 1e-5, act.data_ptr(), rows, k, None)
+    assert call(63, 2048) == -2        # odd rows
+    assert call(12, 2048) == -2        # n = 6 is not a multiple of 8 rows per tile
+    assert call(64, 1024) == -2        # k below 2048
+    assert call(64, 2048) == 0
+    torch.cuda.synchronize()
