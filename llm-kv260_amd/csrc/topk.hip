@@ -40,33 +40,51 @@ __device__ __forceinline__ unsigned long long topk_key(float v, int i) {
 }
 
 __device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
-__device__ __forceinline__ unsigned long long min_u64(unsigned long long a, unsigned long long b) { return a < b ? a : b; }
+
+// The value of lane l ^ S for one 32-bit word: DPP for S = 1, 2, 8 (quad
+// permutations, a rotation by 8 within a row of 16), an LDS swizzle in
+// bit mode for S = 4, 16, ds_bpermute for S = 32.
+template <int S>
+__device__ __forceinline__ int xor_lane(int v, int lane) {
+    if constexpr (S == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    else if constexpr (S == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    else if constexpr (S == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    else if constexpr (S == 4 || S == 16) return __builtin_amdgcn_ds_swizzle(v, (S << 10) | 0x1F);
+    else return __builtin_amdgcn_ds_bpermute((lane ^ S) << 2, v);
+}
 
 // One compare-exchange step of a bitonic network over the wave's 64 lanes:
-// the pair (l, l ^ stride) ends ordered descending when `desc`, with the
-// larger key in the lower lane.
-__device__ __forceinline__ unsigned long long cx(unsigned long long v, int lane, int stride, bool desc) {
-    const unsigned long long o = __shfl_xor(v, stride);
-    const bool lower = (lane & stride) == 0;
-    return lower == desc ? max_u64(v, o) : min_u64(v, o);
+// the pair (l, l ^ S) ends ordered descending when `desc`, with the larger
+// key in the lower lane.
+template <int S>
+__device__ __forceinline__ unsigned long long cx(unsigned long long v, int lane, bool desc) {
+    const int lo = xor_lane<S>((int)(uint32_t)v, lane), hi = xor_lane<S>((int)(uint32_t)(v >> 32), lane);
+    const unsigned long long o = ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+    const bool lower = (lane & S) == 0;
+    return (o > v) == (lower == desc) ? o : v;
+}
+
+template <int SIZE, int S>
+__device__ __forceinline__ unsigned long long sort_steps(unsigned long long v, int lane) {
+    v = cx<S>(v, lane, SIZE == 64 || (lane & SIZE) == 0);
+    if constexpr (S > 1) v = sort_steps<SIZE, S / 2>(v, lane);
+    return v;
 }
 
 // Sort one key per lane into descending order across the wave.
 __device__ __forceinline__ unsigned long long sort64(unsigned long long v, int lane) {
-#pragma unroll
-    for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) v = cx(v, lane, stride, (lane & size) == 0 || size == 64);
-    return v;
+    v = sort_steps<2, 1>(v, lane);
+    v = sort_steps<4, 2>(v, lane);
+    v = sort_steps<8, 4>(v, lane);
+    v = sort_steps<16, 8>(v, lane);
+    v = sort_steps<32, 16>(v, lane);
+    return sort_steps<64, 32>(v, lane);
 }
 
 // The 64 best of two descending lists, one key per lane: lane l keeps
 // max(a[l], b[63 - l]), then the bitonic merge sorts it descending.
 __device__ __forceinline__ unsigned long long merge64(unsigned long long a, unsigned long long b_rev, int lane) {
-    unsigned long long v = max_u64(a, b_rev);
-#pragma unroll
-    for (int stride = 32; stride > 0; stride >>= 1) v = cx(v, lane, stride, true);
-    return v;
+    return sort_steps<64, 32>(max_u64(a, b_rev), lane);
 }
 
 __global__ __launch_bounds__(256) void topk_stage1(const float *__restrict__ y, int n,
