@@ -430,14 +430,10 @@ template <int MT, int D, int OCC>
 hipError_t launch_geo(const GemmParams &Pm, hipStream_t stream) {
     using G = Geo<MT, D, DEPTH, OCC>;
     const void *fn = reinterpret_cast<const void *>(&gemm_mfma_kernel<MT, D, DEPTH, OCC>);
-    static bool lds_allowed = false;
-    if (!lds_allowed) {
-        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_MAX);
-        if (e != hipSuccess) return e;
-        lds_allowed = true;
-    }
+    hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
+    if (e != hipSuccess) return e;
     int per_cu = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, G::LDS);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, G::LDS);
     if (e != hipSuccess) return e;
     if (per_cu < 1) per_cu = 1;
     const long items = (Pm.rows + NR - 1) / NR;

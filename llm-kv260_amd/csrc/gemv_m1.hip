@@ -34,7 +34,11 @@
 //    the slab, and lane 8r + a of the wave reads term a of chunks 0 .. C-1 of
 //    row r and adds them one by one. The eight lane sums of a row then meet
 //    in a DPP adjacent-pair tree.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "../../include/w4a8.h"
 #include "kernels.h"
@@ -712,19 +716,9 @@ __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2
 
 template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX, bool PAIR = false>
 hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
-    // Dynamic LDS above the default 64 KB must be allowed per kernel once.
-    static bool lds_allowed = false;
-    const void *fn = reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>);
-    if (!lds_allowed) {
-        // What the kernel's static LDS (the argmax flag) leaves of the budget.
-        hipFuncAttributes attr{};
-        hipError_t e = hipFuncGetAttributes(&attr, fn);
-        if (e != hipSuccess) return e;
-        e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(LDS_BUDGET - attr.sharedSizeBytes));
-        if (e != hipSuccess) return e;
-        lds_allowed = true;
-    }
+    const hipError_t e =
+        allow_dynamic_lds(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), LDS_BUDGET);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), dim3(grid), dim3(threads), lds, stream, P);
     return hipGetLastError();
 }
@@ -744,15 +738,35 @@ hipError_t launch_layout(const GemvParams &P, bool plain, int grid, int threads,
 }  // namespace
 
 int device_cu_count() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
+}
+
+hipError_t allow_dynamic_lds(const void *fn, size_t budget) {
+    static std::mutex mu;
+    static std::vector<std::pair<const void *, int>> done;   // (kernel, device) pairs already allowed
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> g(mu);
+    for (const auto &d : done)
+        if (d.first == fn && d.second == dev) return hipSuccess;
+    // What the kernel's static LDS leaves of the budget.
+    hipFuncAttributes attr{};
+    e = hipFuncGetAttributes(&attr, fn);
+    if (e != hipSuccess) return e;
+    if (attr.sharedSizeBytes > budget) return hipErrorInvalidValue;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(budget - attr.sharedSizeBytes));
+    if (e != hipSuccess) return e;
+    done.emplace_back(fn, dev);
+    return hipSuccess;
 }
 
 size_t argmax_workspace_bytes() { return ARGMAX_KEY_OFFSET + 64; }
@@ -852,13 +866,8 @@ hipError_t launch_batch_pass(const BatchParams &B, int max_k, hipStream_t stream
     for (int i = 0; i < B.n; ++i) blocks += batch_blocks(B.e[i].rows, B.e[i].k, B.tiles_per_block);
     if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
     const size_t lds = (size_t)(BATCH_THREADS / 64) * TILE_BYTES + x_lds_bytes(max_k / QK);
-    static bool lds_allowed = false;
-    if (!lds_allowed) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel<ONE_PASS>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BUDGET);
-        if (e != hipSuccess) return e;
-        lds_allowed = true;
-    }
+    const hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(&gemv_batch_kernel<ONE_PASS>), LDS_BUDGET);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(gemv_batch_kernel<ONE_PASS>, dim3((unsigned)blocks), dim3(BATCH_THREADS), lds, stream, B);
     return hipGetLastError();
 }

@@ -43,6 +43,11 @@ constexpr int MAX_K_M1 = 16384;   // LDS-staged activation limit of the M=1 kern
 constexpr int MAX_K_GEMM = 16384;
 
 int device_cu_count();            // of the current device (cached per device)
+// Lets kernel `fn` launch with up to `budget` bytes of LDS in all (its static
+// LDS included) on the current device. The runtime needs this once per
+// kernel and device for dynamic LDS above 64 KB; later calls only look it up.
+// Thread-safe.
+hipError_t allow_dynamic_lds(const void *fn, size_t budget);
 
 // argmax != null: also *argmax = the first row of the largest y, reduced in the
 // same launch through `workspace` (argmax_workspace_bytes(), zero between

@@ -221,13 +221,8 @@ hipError_t launch_rmsnorm_q8_0(const float *x, const float *w, float eps, int k,
                                hipStream_t stream) {
     if (m <= 0) return hipSuccess;
     const size_t lds = (size_t)k * 8;                       // float64 squares: 128 KB at k = 16384
-    static bool lds_allowed = false;
-    if (!lds_allowed) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&rmsnorm_q8_0_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
-        if (e != hipSuccess) return e;
-        lds_allowed = true;
-    }
+    const hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(&rmsnorm_q8_0_kernel), 128 * 1024);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rmsnorm_q8_0_kernel, dim3((unsigned)m), dim3(256), lds, stream, x, w, eps, k, out);
     return hipGetLastError();
 }

@@ -177,19 +177,15 @@ hipError_t launch_topk(const float *y, int n, int k, float *vals, int32_t *idx, 
     const int nlists = (n + TOPK_SLICE - 1) / TOPK_SLICE;
     if (n < 1 || nlists > TOPK_MAX_LISTS || k < 1 || k > TOPK_LIST) return hipErrorInvalidValue;
     auto *lists = static_cast<unsigned long long *>(workspace);
+    hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(&topk_stage2),
+                                     (size_t)TOPK_MAX_LISTS * TOPK_LIST * sizeof(unsigned long long));
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(topk_stage1, dim3((unsigned)nlists), dim3(256), 0, stream, y, n, lists);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     int np = 1;
     while (np < nlists) np <<= 1;
     const size_t lds = (size_t)np * TOPK_LIST * sizeof(unsigned long long);
-    static bool lds_allowed = false;
-    if (!lds_allowed) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&topk_stage2), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)((size_t)TOPK_MAX_LISTS * TOPK_LIST * sizeof(unsigned long long)));
-        if (e != hipSuccess) return e;
-        lds_allowed = true;
-    }
     hipLaunchKernelGGL(topk_stage2, dim3(1), dim3(1024), lds, stream, y, lists, nlists, k, vals, idx);
     return hipGetLastError();
 }
