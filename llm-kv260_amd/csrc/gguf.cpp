@@ -134,7 +134,10 @@ int parse(w4a8_gguf &g) {
     g.version = r.u32();
     if (g.version != 2 && g.version != 3) return W4A8_ERR_FORMAT;   // v1 counted in u32
     const uint64_t n_tensors = r.u64(), n_kv = r.u64();
-    if (r.bad || n_kv > g.size || n_tensors > g.size) return W4A8_ERR_FORMAT;
+    // Each key/value takes at least 13 bytes of the file (key length, one
+    // byte of value, type) and each tensor info at least 32, so larger counts
+    // cannot fit: refuse them before reserving anything.
+    if (r.bad || n_kv > g.size / 13 || n_tensors > g.size / 32) return W4A8_ERR_FORMAT;
     g.kv.reserve((size_t)n_kv);
     for (uint64_t i = 0; i < n_kv; ++i) {
         Kv e;
@@ -217,7 +220,12 @@ int w4a8_gguf_open(const char *path, w4a8_gguf **out) {
     }
     g->map = static_cast<const uint8_t *>(m);
     g->size = (size_t)st.st_size;
-    const int s = parse(*g);
+    int s;
+    try {
+        s = parse(*g);
+    } catch (const std::bad_alloc &) {   // names or tables too large for memory: no exception crosses the C ABI
+        s = W4A8_ERR_FORMAT;
+    }
     if (s != W4A8_OK) {
         w4a8_gguf_close(g);
         return s;

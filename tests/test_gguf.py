@@ -104,3 +104,8 @@ def test_malformed_files_are_refused(tmp_path):
     # alignment that is not a power of two
     blob3, _, _ = gguf_bytes([("general.alignment", UINT32, 48)], [], alignment=32)
     refused(blob3)
+    # counts the file cannot hold: refused before anything is reserved for them
+    huge = (1 << 62).to_bytes(8, "little")
+    refused(blob[:8] + huge + blob[16:])                      # tensor count
+    refused(blob[:16] + huge + blob[24:])                     # key/value count
+    refused(blob[:8] + (len(blob) // 32 + 1).to_bytes(8, "little") + blob[16:])
