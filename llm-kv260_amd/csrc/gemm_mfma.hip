@@ -476,6 +476,10 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
 
 }  // namespace
 
+#ifndef W4A8_ROWS_MIN
+#define W4A8_ROWS_MIN 8192
+#endif
+
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hipStream_t stream) {
     // One token is the M = 1 GEMV, byte for byte by the contract, and faster.
     if (m == 1) return launch_gemv_m1(w, x, X_ENGINE, y, stream);
@@ -490,11 +494,12 @@ hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hi
     if ((size_t)P.rows * (size_t)(P.k / QK * Q4_0_BYTES) >= 0x7fff0000u ||
         (size_t)64 * P.rows * 4 >= 0x7fff0000u)
         return hipErrorInvalidValue;
+    const bool by_rows = P.rows >= W4A8_ROWS_MIN && gemm_rows_fits(P.rows, P.k);
     for (int m0 = 0; m0 < m; m0 += 64) {
         P.x = x + (size_t)m0 * P.x_stride;
         P.y = y + (size_t)m0 * P.rows;
         P.m = m - m0 < 64 ? m - m0 : 64;
-        const hipError_t e = launch_tokens(P, stream);
+        const hipError_t e = by_rows ? launch_gemm_rows(P.w, P.x, P.m, P.y, P.rows, P.k, stream) : launch_tokens(P, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -1,0 +1,387 @@
+// Batched W4A8 (M > 1) for matrices with many rows: the same results as
+// gemm_mfma.hip (the contract's order, src/llm_kv260/q4_0.py:170-182, applied
+// row by row), with the work cut along rows instead of along the blocks of K.
+//
+// A 16-row group belongs to a pair of waves for the whole of K. Wave h of the
+// pair owns the contract's accumulators 4h .. 4h + 3: it takes the blocks b
+// with b % 8 in that range, in increasing b, and adds each term to accumulator
+// b % 8 from +0.0f. At the end the pair meets once: wave 0's
+// (a0 + a1) + (a2 + a3) plus wave 1's (a4 + a5) + (a6 + a7) is the
+// adjacent-pair tree's last add. A workgroup holds four pairs (64 rows), so a
+// matrix of N rows has N / 64 workgroups and every wave has the same work.
+//
+// K goes by segments of 512 values (16 blocks). Per segment a pair stages its
+// 16 rows' 288-byte runs in a slab of its own, and the workgroup stages the
+// tokens' 512 activation bytes and 16 scales once for all four pairs: one
+// barrier per segment, with the loads of the next two segments in flight.
+//
+// The integer part is v_mfma_i32_16x16x32_i8 as in gemm_mfma.hip (K = 32 is
+// one block; unsigned nibbles, then a second MFMA against a constant -8
+// operand). Operand layout of the 16x16x32 i8 MFMA (64 lanes):
+//   A: lane l holds A[i = l % 16][k = 8 (l / 16) .. + 7]      (token i)
+//   B: lane l holds B[k = 8 (l / 16) .. + 7][j = l % 16]      (row j)
+//   D: lane l holds D[i = 4 (l / 16) + r][j = l % 16], r = 0..3
+#include "kernels.h"
+#include "q4_0_device.h"
+
+namespace w4a8 {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#ifndef W4A8_ROWS_PAIRS
+#define W4A8_ROWS_PAIRS 4
+#endif
+constexpr int PAIRS = W4A8_ROWS_PAIRS;            // 16-row groups per workgroup
+constexpr int RTHREADS = 64 * 2 * PAIRS;
+constexpr int SEG = 512;                          // activation values per segment
+constexpr int SEG_BLOCKS = SEG / QK;              // 16
+constexpr int SEG_ROW_BYTES = SEG_BLOCKS * Q4_0_BYTES;   // 288
+constexpr int W_PIECES = 16 * SEG_ROW_BYTES / 16;        // 288 pieces of 16 B per pair and segment
+constexpr int SW = (W_PIECES + 127) / 128;                // 3 load slots per thread of a pair
+constexpr int WPITCH = SEG_ROW_BYTES + 16;                // slab row pitch (16-byte aligned)
+constexpr int SLAB = 16 * WPITCH;                         // 4,864 B
+constexpr int OUT_OF_RANGE = 0x7ffffff0;
+constexpr uint32_t BUFFER_DWORD3 = 0x00020000;
+constexpr int CACHE_NT = 2;
+constexpr int LDS_MAX = 160 * 1024;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, BUFFER_DWORD3);
+}
+
+__device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+// DPP quad broadcast of lane R of each quad; folds into the consuming multiply.
+template <int R>
+__device__ __forceinline__ float bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), R * 0x55, 0xF, 0xF, true));
+}
+
+struct RowsParams {
+    const uint8_t *w;
+    const uint8_t *x;      // m rows, engine layout
+    float *y;              // [m][rows]
+    int rows;
+    int k;
+    int m;
+    int x_stride;          // k + k / 8
+};
+
+template <int MT>
+struct RGeo {
+    static constexpr int TT = 16 * MT;                       // tokens
+    static constexpr int APITCH = SEG + 16;                  // int8 bytes per token and segment, padded
+    static constexpr int XDP = TT + 4;                       // scale rows: [16 blocks][XDP]
+    static constexpr int XD_OFF = TT * APITCH;
+    static constexpr int XBUF = XD_OFF + SEG_BLOCKS * XDP * 4;
+    static constexpr int SLAB_OFF = 2 * XBUF;                // [2][PAIRS] slabs
+    static constexpr int EX_OFF = SLAB_OFF + 2 * PAIRS * SLAB;   // pair exchange [PAIRS][TT][16] floats
+    static constexpr int LDS = EX_OFF + PAIRS * TT * 16 * 4;
+    static_assert(LDS <= LDS_MAX, "LDS budget");
+    static constexpr int X_PIECES = TT * (SEG / 16);         // int8 pieces per segment
+    static constexpr int D_PIECES = TT * (SEG_BLOCKS / 4);   // scale pieces (4 scales each)
+    static constexpr int SX = (X_PIECES + RTHREADS - 1) / RTHREADS;
+    static constexpr int SD = (D_PIECES + RTHREADS - 1) / RTHREADS;
+};
+
+template <int MT>
+struct RowsKernel {
+    using G = RGeo<MT>;
+
+    struct Regs {
+        u32x4 w[SW];
+        u32x4 x[G::SX];
+        u32x4 d[G::SD];
+    };
+
+    // Fixed per-thread offsets: weight pieces of the pair's rows, activation
+    // and scale pieces of the workgroup's tokens.
+    struct Slots {
+        uint32_t w_go[SW];
+        int w_lo[SW];          // slab byte offset, -1 for no piece
+        uint32_t x_go[G::SX];
+        int x_lo[G::SX];
+        uint32_t d_go[G::SD];
+        int d_lo[G::SD];       // float index of the piece's first scale in a buffer
+    };
+
+    static __device__ __forceinline__ void slots(const RowsParams &P, int row_bytes, Slots &s) {
+        const int tid = threadIdx.x;
+        const int tp = tid & 127;                // thread within the pair
+#pragma unroll
+        for (int i = 0; i < SW; ++i) {
+            const int n = tp + 128 * i;
+            const int r = n / 18, q = n - 18 * (n / 18);
+            const bool has = n < W_PIECES;
+            s.w_go[i] = has ? (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)q : (uint32_t)OUT_OF_RANGE;
+            s.w_lo[i] = has ? r * WPITCH + 16 * q : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i) {
+            const int n = tid + RTHREADS * i;
+            const int t = n / 32, p = n - 32 * t;
+            const bool has = n < G::X_PIECES;
+            s.x_go[i] = has ? (uint32_t)t * (uint32_t)P.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.x_lo[i] = has ? t * G::APITCH + 16 * p : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i) {
+            const int n = tid + RTHREADS * i;
+            const int p = n / G::TT, t = n - G::TT * p;   // tokens fastest: the transposing writes spread over banks
+            const bool has = n < G::D_PIECES;
+            s.d_go[i] = has ? (uint32_t)t * (uint32_t)P.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.d_lo[i] = has ? G::XD_OFF / 4 + 4 * p * G::XDP + t : -1;
+        }
+    }
+
+    // Loads of segment sg (sg >= nseg: nothing; the resources are then empty).
+    static __device__ __forceinline__ void load(const RowsParams &P, const Slots &s, int row_bytes, int n0, int sg,
+                                                int nseg, Regs &rg) {
+        const bool live = sg < nseg;
+        const uint32_t rows_left = n0 < P.rows ? (uint32_t)(P.rows - n0) : 0u;
+        const uint32_t w_skip = (uint32_t)sg * SEG_ROW_BYTES;
+        const __amdgpu_buffer_rsrc_t wb =
+            rsrc(P.w + (size_t)n0 * row_bytes + (live ? w_skip : 0u),
+                 live && rows_left ? rows_left * (uint32_t)row_bytes - w_skip : 0u);
+        const uint32_t xs = (uint32_t)P.m * (uint32_t)P.x_stride;
+        const __amdgpu_buffer_rsrc_t xb = rsrc(P.x + (live ? sg * SEG : 0), live ? xs - (uint32_t)(sg * SEG) : 0u);
+        const uint32_t d0 = (uint32_t)P.k + (uint32_t)sg * SEG_BLOCKS * 4u;
+        const __amdgpu_buffer_rsrc_t db = rsrc(P.x + (live ? d0 : 0u), live ? xs - d0 : 0u);
+#pragma unroll
+        for (int i = 0; i < SW; ++i) rg.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wb, (int)s.w_go[i], 0, CACHE_NT);
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i) rg.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xb, (int)s.x_go[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i) rg.d[i] = __builtin_amdgcn_raw_buffer_load_b128(db, (int)s.d_go[i], 0, 0);
+    }
+
+    static __device__ __forceinline__ void stage(uint8_t *xbuf, uint8_t *slab, const Slots &s, const Regs &rg) {
+#pragma unroll
+        for (int i = 0; i < SW; ++i)
+            if (s.w_lo[i] >= 0) *reinterpret_cast<u32x4 *>(slab + s.w_lo[i]) = rg.w[i];
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i)
+            if ((i + 1) * RTHREADS <= G::X_PIECES || s.x_lo[i] >= 0)
+                *reinterpret_cast<u32x4 *>(xbuf + s.x_lo[i]) = rg.x[i];
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i)
+            if ((i + 1) * RTHREADS <= G::D_PIECES || s.d_lo[i] >= 0) {
+                uint32_t *xd = reinterpret_cast<uint32_t *>(xbuf) + s.d_lo[i];
+                const u32x4 v = rg.d[i];
+                xd[0] = v.x;
+                xd[G::XDP] = v.y;
+                xd[2 * G::XDP] = v.z;
+                xd[3 * G::XDP] = v.w;
+            }
+    }
+
+    // Block B (0..15) of the segment: its MFMA sums for every token tile.
+    template <int B>
+    static __device__ __forceinline__ void block_sums(const uint8_t *slab, const uint8_t *xbuf, int j, int g, v4i v[MT],
+                                                      float &dw, float dx[MT]) {
+        const int h = g & 1;
+        const int shift = (g >> 1) * 4;
+        const uint8_t *wrow = slab + j * WPITCH + 18 * B;
+        uint32_t lo, hi, d_bits;
+        if constexpr ((B & 1) == 0) {
+            // Dword-aligned block: scale in the low half, the nibble run two bytes in.
+            const uint32_t *run = reinterpret_cast<const uint32_t *>(wrow + 8 * h);
+            const uint32_t v0 = run[0], v1 = run[1], v2 = run[2];
+            lo = __builtin_amdgcn_alignbyte(v1, v0, 2);
+            hi = __builtin_amdgcn_alignbyte(v2, v1, 2);
+            d_bits = *reinterpret_cast<const uint32_t *>(wrow) & 0xFFFFu;
+        } else {
+            // Two bytes into a dword: scale in the high half of the dword before, the run aligned.
+            const uint32_t *run = reinterpret_cast<const uint32_t *>(wrow + 2 + 8 * h);
+            lo = run[0];
+            hi = run[1];
+            d_bits = *reinterpret_cast<const uint32_t *>(wrow - 2) >> 16;
+        }
+        const long bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
+        const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
+        dw = half_bits_to_float(d_bits);
+        const uint8_t *xa = xbuf + j * G::APITCH + 32 * B + 8 * g;
+        const float *xs = reinterpret_cast<const float *>(xbuf + G::XD_OFF) + B * G::XDP + 4 * g + (j & 3);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
+            dx[t] = xs[16 * t];
+            v4i z = {0, 0, 0, 0};
+            z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+            v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
+        }
+    }
+
+    // The terms of NB consecutive blocks B0 .. B0 + NB - 1 (accumulators
+    // B0 % 4 ..), in block order: their MFMAs first, then the fp32 terms.
+    template <int B0, int NB>
+    static __device__ __forceinline__ void blocks(const uint8_t *slab, const uint8_t *xbuf, int j, int g,
+                                                  float acc[4][MT][4]) {
+        v4i v[NB][MT];
+        float dw[NB], dx[NB][MT];
+        block_sums<B0>(slab, xbuf, j, g, v[0], dw[0], dx[0]);
+        block_sums<B0 + 1>(slab, xbuf, j, g, v[1], dw[1], dx[1]);
+        if constexpr (NB == 4) {
+            block_sums<B0 + 2>(slab, xbuf, j, g, v[2], dw[2], dx[2]);
+            block_sums<B0 + 3>(slab, xbuf, j, g, v[3], dw[3], dx[3]);
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const float dxs[4] = {bcast<0>(dx[c][t]), bcast<1>(dx[c][t]), bcast<2>(dx[c][t]), bcast<3>(dx[c][t])};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a = (float)v[c][t][r] * dw[c];
+                    acc[(B0 + c) & 3][t][r] = acc[(B0 + c) & 3][t][r] + a * dxs[r];
+                }
+            }
+    }
+
+    // The wave's eight blocks of a segment: its four accumulators' blocks
+    // 4 half + c, then 8 + 4 half + c, in order. Two blocks per phase at four
+    // token tiles keeps the MFMA results within the register budget.
+    template <int H>
+    static __device__ __forceinline__ void segment(const uint8_t *slab, const uint8_t *xbuf, int j, int g,
+                                                   float acc[4][MT][4]) {
+        if constexpr (MT <= 2) {
+            blocks<4 * H, 4>(slab, xbuf, j, g, acc);
+            blocks<8 + 4 * H, 4>(slab, xbuf, j, g, acc);
+        } else {
+            blocks<4 * H, 2>(slab, xbuf, j, g, acc);
+            blocks<4 * H + 2, 2>(slab, xbuf, j, g, acc);
+            blocks<8 + 4 * H, 2>(slab, xbuf, j, g, acc);
+            blocks<8 + 4 * H + 2, 2>(slab, xbuf, j, g, acc);
+        }
+    }
+
+    static __device__ __forceinline__ void run(const RowsParams &P, uint8_t *lds) {
+        const int tid = threadIdx.x;
+        // The wave index is uniform: as a scalar, the pair's resources and the
+        // choice of accumulators are scalar too (no per-lane resource loop).
+        const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int pair = wave >> 1, half = wave & 1;
+        const int j = lane & 15, g = lane >> 4;
+        const int row_bytes = P.k / QK * Q4_0_BYTES;
+        const int nseg = P.k / SEG;
+        const int n0 = ((int)blockIdx.x * PAIRS + pair) * 16;   // the pair's first row
+
+        Slots s;
+        slots(P, row_bytes, s);
+        // Segments in flight: two; one at four token tiles, whose segment
+        // takes long enough to cover the loads of the next and whose
+        // registers are needed for the MFMA results.
+        constexpr int DEPTH = MT >= 4 ? 1 : 2;
+        Regs rg[DEPTH];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(P, s, row_bytes, n0, d, nseg, rg[d]);
+        stage(lds, lds + G::SLAB_OFF + pair * SLAB, s, rg[0]);
+        load(P, s, row_bytes, n0, DEPTH, nseg, rg[0]);
+        __syncthreads();
+
+        float acc[4][MT][4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[c][t][r] = 0.0f;
+
+        for (int sg0 = 0; sg0 < nseg; sg0 += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                const int sg = sg0 + d;
+                if (sg < nseg) {
+                    const uint8_t *xbuf = lds + (sg & 1) * G::XBUF;
+                    const uint8_t *slab = lds + G::SLAB_OFF + ((sg & 1) * PAIRS + pair) * SLAB;
+                    if (half == 0)
+                        segment<0>(slab, xbuf, j, g, acc);
+                    else
+                        segment<1>(slab, xbuf, j, g, acc);
+                }
+                // Segment sg + 1 into the other buffers (last read for
+                // segment sg - 1, before the previous barrier); its registers
+                // then take segment sg + 1 + DEPTH.
+                const int nx = sg + 1;
+                stage(lds + (nx & 1) * G::XBUF, lds + G::SLAB_OFF + ((nx & 1) * PAIRS + pair) * SLAB, s,
+                      rg[(d + 1) % DEPTH]);
+                load(P, s, row_bytes, n0, nx + DEPTH, nseg, rg[(d + 1) % DEPTH]);
+                __syncthreads();
+            }
+        }
+
+        // The pair meets: wave 1 hands (a4 + a5) + (a6 + a7) to wave 0.
+        float *ex = reinterpret_cast<float *>(lds + G::EX_OFF) + pair * G::TT * 16;
+        float part[MT][4];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[t][r] = (acc[0][t][r] + acc[1][t][r]) + (acc[2][t][r] + acc[3][t][r]);
+        if (half == 1) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ex[(16 * t + 4 * g + r) * 16 + j] = part[t][r];
+        }
+        __syncthreads();
+        if (half == 0) {
+            const uint32_t y_bytes = (uint32_t)P.m * (uint32_t)P.rows * 4u;
+            const __amdgpu_buffer_rsrc_t yb = rsrc(P.y, y_bytes);
+            const bool row_ok = n0 + j < P.rows;
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tok = 16 * t + 4 * g + r;
+                    const float yv = part[t][r] + ex[tok * 16 + j];
+                    const bool ok = row_ok && tok < P.m;
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(yv), yb, ok ? (int)(((uint32_t)tok * (uint32_t)P.rows + (uint32_t)(n0 + j)) * 4u) : OUT_OF_RANGE,
+                        0, 0);
+                }
+        }
+    }
+};
+
+template <int MT>
+__global__ __launch_bounds__(RTHREADS) void gemm_rows_kernel(RowsParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    RowsKernel<MT>::run(P, lds);
+}
+
+template <int MT>
+hipError_t launch_rows_mt(const RowsParams &P, hipStream_t stream) {
+    const void *fn = reinterpret_cast<const void *>(&gemm_rows_kernel<MT>);
+    const hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
+    if (e != hipSuccess) return e;
+    const int grid = (P.rows + 16 * PAIRS - 1) / (16 * PAIRS);
+    hipLaunchKernelGGL(gemm_rows_kernel<MT>, dim3((unsigned)grid), dim3(RTHREADS), RGeo<MT>::LDS, stream, P);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_rows_fits(int rows, int k) {
+    return k % SEG == 0 && (size_t)rows * (size_t)(k / QK * Q4_0_BYTES) < 0x7fff0000u;
+}
+
+// m <= 64 tokens; y is [m][rows].
+hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y, int rows, int k, hipStream_t stream) {
+    if (m < 1 || m > 64 || !gemm_rows_fits(rows, k)) return hipErrorInvalidValue;
+    RowsParams P{};
+    P.w = w;
+    P.x = x;
+    P.y = y;
+    P.rows = rows;
+    P.k = k;
+    P.m = m;
+    P.x_stride = k + k / 8;
+    if (m <= 16) return launch_rows_mt<1>(P, stream);
+    if (m <= 32) return launch_rows_mt<2>(P, stream);
+    return launch_rows_mt<4>(P, stream);
+}
+
+}  // namespace w4a8

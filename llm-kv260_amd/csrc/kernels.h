@@ -67,6 +67,9 @@ int topk_max_n();
 
 // y[m][rows] for m activation rows in engine layout (row stride K + K/8 bytes).
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, float *y, hipStream_t stream);
+// The row-split M > 1 kernel (gemm_rows.hip): m <= 64, k % 512 == 0.
+bool gemm_rows_fits(int rows, int k);
+hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y, int rows, int k, hipStream_t stream);
 
 // x: float32[m][K] -> engine layout rows, or ggml Q8_0 block rows.
 hipError_t launch_quantize_q8_0(const float *x, int k, int m, uint8_t *out, XFormat out_fmt, hipStream_t stream);

@@ -210,7 +210,12 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       (24, 512, 2048), (33, 80, 1024), (64, 128, 2048),
                                       # one chunk per row; three and five chunks (rounds of one chunk);
                                       # several 64-token groups; one row
-                                      (8, 16, 256), (40, 33, 768), (130, 40, 1280), (2, 1, 512)])
+                                      (8, 16, 256), (40, 33, 768), (130, 40, 1280), (2, 1, 512),
+                                      # 8192 rows and more go to the row-split kernel: ragged row
+                                      # groups and workgroups, one to three token tiles, several
+                                      # 64-token groups, one to four K segments
+                                      (3, 8200, 512), (17, 8208, 1024), (40, 8240, 2048), (64, 8192, 512),
+                                      (130, 8256, 1536)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
