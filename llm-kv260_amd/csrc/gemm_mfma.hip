@@ -324,7 +324,9 @@ struct Kernel {
         const int C = Pm.k >> 8;
         const int RPI = C / D;                                  // rounds per item (D divides C)
         const int row_bytes = C * CHUNK_BYTES;
-        const int items = (Pm.rows + NR - 1) / NR;
+        // Items are (row group, token group) pairs, row groups fastest.
+        const int row_groups = (Pm.rows + NR - 1) / NR;
+        const int items = row_groups * ((Pm.m + G::TT - 1) / G::TT);
         const int GD = gridDim.x;
         const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / GD + 1 : 0;
         const int QP = (my_items * RPI + P - 1) / P * P;        // rounds, padded to whole groups of P
@@ -332,24 +334,40 @@ struct Kernel {
         Slots s;
         slots(Pm, row_bytes, s);
 
-        auto load_at = [&](int kk, int ss, R &rg) {
-            load(Pm, s, row_bytes, ((int)blockIdx.x + kk * GD) * NR, 0, ss * D, kk < my_items, rg);
+        // A position in the workgroup's stream: round ss of its item kk, whose
+        // row group and token group are rg_i and tg_i. Items kk and kk + 1
+        // are GD apart, so moving to the next item adds GD to the row group
+        // and carries into the token group (a few steps: GD <= items).
+        struct Pos {
+            int kk, ss, rg_i, tg_i;
         };
-        auto advance = [&](int &kk, int &ss) {
-            if (++ss == RPI) {
-                ss = 0;
-                ++kk;
+        auto advance = [&](Pos &p) {
+            if (++p.ss == RPI) {
+                p.ss = 0;
+                ++p.kk;
+                p.rg_i += GD;
+                while (p.rg_i >= row_groups) {
+                    p.rg_i -= row_groups;
+                    ++p.tg_i;
+                }
             }
         };
+        auto load_at = [&](const Pos &p, R &rg) {
+            load(Pm, s, row_bytes, p.rg_i * NR, p.tg_i * G::TT, p.ss * D, p.kk < my_items, rg);
+        };
+        const Pos first{0, 0, (int)blockIdx.x % row_groups, (int)blockIdx.x / row_groups};
         const uint32_t y_total = (uint32_t)((size_t)Pm.m * Pm.rows * 4);
 
         R rg[P];
+        Pos lp = first;                                         // the load position
 #pragma unroll
-        for (int d = 0; d < P; ++d) load_at(d / RPI, d % RPI, rg[d]);
+        for (int d = 0; d < P; ++d) {
+            load_at(lp, rg[d]);
+            advance(lp);
+        }
         stage(lds, s, rg[0]);
-        int lk = P / RPI, ls = P % RPI;                         // the load position: round P
-        load_at(lk, ls, rg[0]);
-        advance(lk, ls);
+        load_at(lp, rg[0]);                                     // round P
+        advance(lp);
         __syncthreads();
 
         float acc[MT][4];
@@ -358,15 +376,15 @@ struct Kernel {
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
 
-        int ck = 0, cs = 0;                                     // the compute position: round q
+        Pos cp = first;                                         // the compute position: round q
         for (int q0 = 0; q0 < QP; q0 += P) {
 #pragma unroll
             for (int d = 0; d < P; ++d) {
                 const int q = q0 + d;
-                const bool live = ck < my_items;
-                const bool item_end = live && cs == RPI - 1;
-                const int n0 = ((int)blockIdx.x + ck * GD) * NR;
-                float *ex = reinterpret_cast<float *>(lds + G::EX_OFF + (G::EXN == 2 ? (ck & 1) * G::EX_BYTES : 0));
+                const bool live = cp.kk < my_items;
+                const bool item_end = live && cp.ss == RPI - 1;
+                const int n0 = cp.rg_i * NR, m0 = cp.tg_i * G::TT;
+                float *ex = reinterpret_cast<float *>(lds + G::EX_OFF + (G::EXN == 2 ? (cp.kk & 1) * G::EX_BYTES : 0));
                 if (live) compute(lds + (q & 1) * G::BUF, acc);
                 if (item_end) {
 #pragma unroll
@@ -381,14 +399,14 @@ struct Kernel {
                 // before the previous barrier), then its registers take round
                 // q + 1 + P.
                 stage(lds + ((q + 1) & 1) * G::BUF, s, rg[(d + 1) % P]);
-                load_at(lk, ls, rg[(d + 1) % P]);
-                advance(lk, ls);
+                load_at(lp, rg[(d + 1) % P]);
+                advance(lp);
                 __syncthreads();
                 // At an item's end: the eight accumulators of each output meet
                 // in the adjacent-pair tree. Every thread issues its stores in
                 // every round; the resource is empty when there is nothing to
                 // store, and a lane past M or N stores out of range.
-                const uint32_t y0 = (uint32_t)n0 * 4u;
+                const uint32_t y0 = ((uint32_t)m0 * (uint32_t)Pm.rows + (uint32_t)n0) * 4u;
                 const __amdgpu_buffer_rsrc_t yb =
                     buffer_of(reinterpret_cast<uint8_t *>(Pm.y) + y0, item_end ? y_total - y0 : 0u);
 #pragma unroll
@@ -400,12 +418,12 @@ struct Kernel {
                         for (int a = 0; a < 8; ++a) l[a] = ex[a * G::TT * G::EXP + s.o_ex[o]];
                         yv = ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]));
                     }
-                    const bool ok = s.o_tok[o] < Pm.m && s.o_row[o] < Pm.rows - n0;
+                    const bool ok = s.o_tok[o] < Pm.m - m0 && s.o_row[o] < Pm.rows - n0;
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), yb, ok ? (int)s.o_y[o] : OUT_OF_RANGE,
                                                           0, 0);
                 }
                 if (G::EXN == 1 && item_end) __syncthreads();   // the exchange is read before it is written again
-                advance(ck, cs);
+                advance(cp);
             }
         }
     }
@@ -436,7 +454,7 @@ hipError_t launch_geo(const GemmParams &Pm, hipStream_t stream) {
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, G::LDS);
     if (e != hipSuccess) return e;
     if (per_cu < 1) per_cu = 1;
-    const long items = (Pm.rows + NR - 1) / NR;
+    const long items = (long)((Pm.rows + NR - 1) / NR) * ((Pm.m + G::TT - 1) / G::TT);
     long grid = (long)device_cu_count() * per_cu;
     if (grid > items) grid = items;
     hipLaunchKernelGGL((gemm_mfma_kernel<MT, D, DEPTH, OCC>), dim3((unsigned)grid), dim3(GTHREADS), G::LDS, stream, Pm);
@@ -464,13 +482,25 @@ hipError_t launch_mt(const GemmParams &Pm, hipStream_t stream) {
 #define W4A8_GEMM_OCC 2
 #endif
 
+#ifndef W4A8_GEMM_SPLIT_ITEMS
+#define W4A8_GEMM_SPLIT_ITEMS 160
+#endif
+
 hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
-    // 16, 32 or 64 tokens per item (all of M up to 64, so the weights stream
-    // once); a round holds 128 (or, at two workgroups per CU, 64) token-chunks
-    // of activations.
+    // 16, 32 or 64 tokens per item. The widest tile that covers M streams the
+    // weights once. With few row groups (2,048 rows: o, down) that leaves
+    // most CUs idle, and 16-token items, one per (row group, token group),
+    // are faster: down at M = 64 in 16.9 us against 28.3, at M = 24 in 11.4
+    // against 16.2 (the weights are read once per token group, the later reads
+    // mostly from the caches). At 3,072 rows the wide tile is as fast or
+    // faster. A round holds 128 (or, at two workgroups per CU, 64)
+    // token-chunks of activations.
     constexpr int OCC = W4A8_GEMM_OCC;
-    if (Pm.m <= 16) return launch_mt<1, 8 / OCC, OCC>(Pm, stream);
-    if (Pm.m <= 32) return launch_mt<2, 4 / OCC, OCC>(Pm, stream);
+    const long row_groups = (Pm.rows + NR - 1) / NR;
+    int mt = Pm.m <= 16 ? 1 : Pm.m <= 32 ? 2 : 4;
+    if (mt > 1 && row_groups * ((Pm.m + 16 * mt - 1) / (16 * mt)) < W4A8_GEMM_SPLIT_ITEMS) mt = 1;
+    if (mt == 1) return launch_mt<1, 8 / OCC, OCC>(Pm, stream);
+    if (mt == 2) return launch_mt<2, 4 / OCC, OCC>(Pm, stream);
     return launch_mt<4, 2 / OCC, OCC>(Pm, stream);
 }
 
