@@ -215,7 +215,9 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       # groups and workgroups, one to three token tiles, several
                                       # 64-token groups, one to four K segments
                                       (3, 8200, 512), (17, 8208, 1024), (40, 8240, 2048), (64, 8192, 512),
-                                      (130, 8256, 1536)])
+                                      (130, 8256, 1536),
+                                      # the largest K, on both kernels
+                                      (40, 64, 16384), (5, 8200, 16384)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
