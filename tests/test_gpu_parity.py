@@ -230,6 +230,24 @@ def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     assert_bytes_equal(host(y), want, "gemm")
 
 
+@pytest.mark.parametrize("m,rows,k", [(24, 8200, 1024), (40, 2000, 1024)])
+def test_gemm_random_bytes(gpu, m, rows, k):
+    """Arbitrary block bytes and activations (any finite fp16 scale) through both M > 1
+    kernels (8,200 rows: the row-split one), row by row against the contract."""
+    rng = np.random.default_rng(78 + m)
+    blocks = rng.integers(0, 256, size=(rows, k // 32, 18), dtype=np.uint8)
+    d = (rng.standard_normal((rows, k // 32)) * 10.0 ** rng.integers(-7, 3, (rows, k // 32))).astype(np.float16)
+    blocks[..., :2] = d.view(np.uint8).reshape(rows, k // 32, 2)
+    blocks = blocks.reshape(rows, -1)
+    xq = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    xd = (rng.random((m, k // 32)) * 0.05).astype(np.float16)
+    want = C.gemm_q4_0_rows(blocks, k, xq, xd)
+    x_rows = np.stack([C.pack_x_for_engine(xq[i], xd[i]) for i in range(m)])
+    y = poisoned_f32((m, rows))
+    gpu.gemm_engine(dev(blocks), k, dev(x_rows), out=y)
+    assert_bytes_equal(host(y), want, "gemm, random bytes")
+
+
 def test_gemm_one_row_equals_gemv(gpu):
     rows, k = 96, 2048
     _, _, blocks, xq, xd = _case(rows, k, 130, 131)
