@@ -185,6 +185,33 @@ def test_gemv_random_bytes(gpu):
     assert_bytes_equal(host(y), want)
 
 
+def test_gemv_nonfinite_scales(gpu):
+    """Infinite and NaN fp16 scales: every output the contract leaves finite or infinite is
+    byte-identical; where the contract gives NaN the GPU gives NaN too. (A NaN's sign and
+    payload are the processor's: x86 makes 0 * inf the negative default NaN, the GPU the
+    positive one, so NaN bytes are not compared.)"""
+    rng = np.random.default_rng(91)
+    rows, k = 64, 1024
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 92, 0.02)).reshape(rows, k // 32, 18)
+    specials = np.array([np.inf, -np.inf, np.nan, 65504.0], np.float16)
+    for r in range(0, rows, 2):                      # every other row gets one special scale
+        blocks[r, rng.integers(0, k // 32), :2] = specials[(r // 2) % 4:(r // 2) % 4 + 1].view(np.uint8)
+    blocks[5, :, 2:] = 0x88                           # weights all 8 - 8 = 0 ...
+    blocks[5, 3, :2] = np.array([np.inf], np.float16).view(np.uint8)   # ... so 0 * inf: NaN
+    blocks = blocks.reshape(rows, -1)
+    xq, xd = C.quantize_q8_0(O.normal_f32((1, k), 93)[0])
+    xd = xd.copy()
+    xd[7] = np.float16(np.inf)                        # an infinite activation scale too
+    want = C.gemv_q4_0(blocks, k, xq, xd)
+    y = poisoned_f32(rows)
+    gpu.gemv_engine(dev(blocks), k, dev(C.pack_x_for_engine(xq, xd)), out=y)
+    got = host(y)
+    nan = np.isnan(want)
+    assert nan.any() and np.isinf(want).any()
+    assert np.array_equal(np.isnan(got), nan), np.flatnonzero(np.isnan(got) != nan)
+    assert_bytes_equal(got[~nan], want[~nan], "non-NaN outputs")
+
+
 def test_gemv_quarters_at_separate_addresses(gpu):
     """The v1 engine's layout (gemv_dev_start4): four quarters anywhere in memory."""
     import torch
