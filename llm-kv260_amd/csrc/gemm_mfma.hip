@@ -496,13 +496,15 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
     // most CUs idle, and 16-token items, one per (row group, token group),
     // are faster: down at M = 64 in 16.9 us against 28.3, at M = 24 in 11.4
     // against 16.2 (the weights are read once per token group, the later reads
-    // mostly from the caches). At 3,072 rows the wide tile is as fast or
-    // faster. A round holds 128 (or, at two workgroups per CU, 64)
+    // mostly from the caches). At 3,072 rows (192 row groups) 16-token items
+    // win at M > 32 only (8.8 against 9.5 us at M = 64; at M = 24 the 32-token
+    // tile is faster). A round holds 128 (or, at two workgroups per CU, 64)
     // token-chunks of activations.
     constexpr int OCC = W4A8_GEMM_OCC;
     const long row_groups = (Pm.rows + NR - 1) / NR;
     int mt = Pm.m <= 16 ? 1 : Pm.m <= 32 ? 2 : 4;
-    if (mt > 1 && row_groups * ((Pm.m + 16 * mt - 1) / (16 * mt)) < W4A8_GEMM_SPLIT_ITEMS) mt = 1;
+    const long wide_items = row_groups * ((Pm.m + 16 * mt - 1) / (16 * mt));
+    if (mt > 1 && (wide_items < W4A8_GEMM_SPLIT_ITEMS || (mt == 4 && wide_items < 2 * W4A8_GEMM_SPLIT_ITEMS))) mt = 1;
     if (mt == 1) return launch_mt<1, 8 / OCC, OCC>(Pm, stream);
     if (mt == 2) return launch_mt<2, 4 / OCC, OCC>(Pm, stream);
     return launch_mt<4, 2 / OCC, OCC>(Pm, stream);
