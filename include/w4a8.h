@@ -59,7 +59,7 @@ size_t w4a8_q8_0_row_bytes(int k);
 /* y[rows] = W[rows, k] x, x in the engine layout int8[k] | float32[k/32]
  * (pack_x_for_engine, src/llm_kv260/q4_0.py:193-200). The call the v1 engine
  * made with gemv_dev_run (board/kv260gemv/gemv_dev.h:19-23), now with the
- * north-star argument order gemv(weights, activation, out, rows, cols). */
+ * drop-in argument order gemv(weights, activation, out, rows, cols). */
 int w4a8_gemv(const void *w, const void *x, float *y, int rows, int k, void *stream);
 
 /* Same, x as ggml Q8_0 blocks (34 bytes each: fp16 d then 32 int8). x needs
