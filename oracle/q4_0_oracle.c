@@ -2,7 +2,7 @@
  * CPU oracle (scalar C) for the W4A8 Q4_0 x Q8_0 GEMV contract.
  *
  * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py as the checker. The product library never links
+ * cpu_baseline leg of bench.py, to compare the library against. The product library never links
  * it.
  *
  * A second, independent restatement of src/llm_kv260/q4_0.py (the first is

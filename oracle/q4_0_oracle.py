@@ -1,6 +1,6 @@
 """CPU oracle for the W4A8 (Q4_0 weights x Q8_0 activation) GEMV contract.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker, never the thing that is
+TEST INFRASTRUCTURE ONLY. This module is what the library is compared against, never the thing that is
 measured or shipped: only `tests/`, `__graft_entry__.smoke()` and the
 `cpu_baseline` leg of `bench.py` may import it. The product path (the HIP
 library under `llm-kv260_amd/`) never calls into it and fails loudly when its
