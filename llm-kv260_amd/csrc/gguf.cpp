@@ -13,6 +13,7 @@
 
 #include <new>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/w4a8.h"
@@ -139,9 +140,11 @@ int parse(w4a8_gguf &g) {
     // cannot fit: refuse them before reserving anything.
     if (r.bad || n_kv > g.size / 13 || n_tensors > g.size / 32) return W4A8_ERR_FORMAT;
     g.kv.reserve((size_t)n_kv);
+    std::unordered_set<std::string> keys, names;
     for (uint64_t i = 0; i < n_kv; ++i) {
         Kv e;
-        if (!r.str(&e.key)) return W4A8_ERR_FORMAT;
+        // A name with a NUL byte could not be asked for through the C API.
+        if (!r.str(&e.key) || e.key.find('\0') != std::string::npos) return W4A8_ERR_FORMAT;
         e.type = r.u32();
         e.val = r.p;
         if (e.type == W4A8_GGUF_ARRAY) {
@@ -150,6 +153,7 @@ int parse(w4a8_gguf &g) {
             e.count = peek.u64();
         }
         if (!skip_value(r, e.type, 0)) return W4A8_ERR_FORMAT;
+        if (!keys.insert(e.key).second) return W4A8_ERR_FORMAT;   // a key twice, as llama.cpp refuses too
         if (e.key == "general.alignment") {
             if (e.type != W4A8_GGUF_UINT32) return W4A8_ERR_FORMAT;
             memcpy(&g.alignment, e.val, 4);
@@ -160,7 +164,8 @@ int parse(w4a8_gguf &g) {
     g.tensors.reserve((size_t)n_tensors);
     for (uint64_t i = 0; i < n_tensors; ++i) {
         Tensor t;
-        if (!r.str(&t.name)) return W4A8_ERR_FORMAT;
+        if (!r.str(&t.name) || t.name.find('\0') != std::string::npos) return W4A8_ERR_FORMAT;
+        if (!names.insert(t.name).second) return W4A8_ERR_FORMAT;   // a tensor name twice
         t.n_dims = r.u32();
         if (t.n_dims < 1 || t.n_dims > 4) return W4A8_ERR_FORMAT;
         for (uint32_t d = 0; d < t.n_dims; ++d) t.ne[d] = r.u64();

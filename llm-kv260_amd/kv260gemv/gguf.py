@@ -16,12 +16,23 @@ weight matrix the GEMV entry points read in place.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 
 from . import W4A8Error, lib
 
 GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q4_0, GGML_TYPE_Q8_0 = 0, 1, 2, 8
 ERR_FORMAT = -6
+
+
+def _text(b: bytes) -> str:
+    """Key, name and string bytes as text. GGUF strings are UTF-8; bytes that are
+    not decode to lone surrogates, so every name still round-trips through _raw."""
+    return b.decode("utf-8", "surrogateescape")
+
+
+def _raw(s: str) -> bytes:
+    return s.encode("utf-8", "surrogateescape")
 
 
 class _Tensor(ctypes.Structure):
@@ -88,7 +99,7 @@ class GGUFFile:
     def __init__(self, path: str):
         self._L = _bind()
         h = ctypes.c_void_p()
-        st = self._L.w4a8_gguf_open(str(path).encode(), ctypes.byref(h))
+        st = self._L.w4a8_gguf_open(os.fsencode(str(path)), ctypes.byref(h))
         if st != 0:
             raise W4A8Error("w4a8_gguf_open", st)
         self._h = h
@@ -113,11 +124,11 @@ class GGUFFile:
         return self._L.w4a8_gguf_data_offset(self._h)
 
     def keys(self) -> list:
-        return [self._L.w4a8_gguf_key(self._h, i).decode() for i in range(self._L.w4a8_gguf_n_kv(self._h))]
+        return [_text(self._L.w4a8_gguf_key(self._h, i)) for i in range(self._L.w4a8_gguf_n_kv(self._h))]
 
     def _scalar(self, fn, ctype, key):
         v = ctype()
-        st = getattr(self._L, fn)(self._h, key.encode(), ctypes.byref(v))
+        st = getattr(self._L, fn)(self._h, _raw(key), ctypes.byref(v))
         if st != 0:
             raise KeyError(key) if st == -2 else W4A8Error(fn, st)
         return v.value
@@ -141,13 +152,13 @@ class GGUFFile:
 
     def string(self, key: str) -> str:
         ptr, n = ctypes.c_void_p(), ctypes.c_uint64()
-        st = self._L.w4a8_gguf_get_str(self._h, key.encode(), ctypes.byref(ptr), ctypes.byref(n))
+        st = self._L.w4a8_gguf_get_str(self._h, _raw(key), ctypes.byref(ptr), ctypes.byref(n))
         if st != 0:
             raise KeyError(key) if st == -2 else W4A8Error("w4a8_gguf_get_str", st)
-        return ctypes.string_at(ptr.value, n.value).decode()
+        return _text(ctypes.string_at(ptr.value, n.value))
 
     def kv_type(self, key: str) -> tuple:
-        i = self._L.w4a8_gguf_find_key(self._h, key.encode())
+        i = self._L.w4a8_gguf_find_key(self._h, _raw(key))
         if i < 0:
             raise KeyError(key)
         t, et, n = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
@@ -158,7 +169,7 @@ class GGUFFile:
         return [self._info(i) for i in range(self._L.w4a8_gguf_n_tensors(self._h))]
 
     def _index(self, name: str) -> int:
-        i = self._L.w4a8_gguf_find_tensor(self._h, name.encode())
+        i = self._L.w4a8_gguf_find_tensor(self._h, _raw(name))
         if i < 0:
             raise KeyError(f"tensor {name} missing")
         return i
@@ -168,7 +179,7 @@ class GGUFFile:
         st = self._L.w4a8_gguf_tensor_info(self._h, i, ctypes.byref(t))
         if st != 0:
             raise W4A8Error("w4a8_gguf_tensor_info", st)
-        return TensorInfo(t.name.decode(), t.type, tuple(t.ne[d] for d in range(t.n_dims)), t.offset, t.nbytes)
+        return TensorInfo(_text(t.name), t.type, tuple(t.ne[d] for d in range(t.n_dims)), t.offset, t.nbytes)
 
     def tensor(self, name: str) -> TensorInfo:
         return self._info(self._index(name))
