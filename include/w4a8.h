@@ -123,7 +123,10 @@ int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, 
  * 619, ggml's vector expf) written in place of y: float32[n], the activation
  * of down. Byte-identical to that GEMV followed by silu_mul, with silu
  * computed once per output instead of by every workgroup of down.
- * 2048 <= k <= 8192, n a multiple of 64 / (k / 256). */
+ * 2048 <= k <= 8192, n a multiple of r = 64 / (k / 256) rows (whole tiles of
+ * r rows in each half), and the n / r tiles of each half a multiple of 2 when
+ * k > 2048 and of 4 when k > 4096 (a workgroup holds one thread per
+ * activation block and divides them); other shapes return W4A8_ERR_SHAPE. */
 int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, float eps, float *act, int rows, int k,
                            void *stream);
 
@@ -168,12 +171,44 @@ typedef struct w4a8_chain_step {
 
 /* A token's matrices in order (board/tp/tp_llama.cpp:822-883: per layer
  * q|k|v, o, gate|up, down, then the LM head; 65 engine calls per token).
- * Step j does not start its dot products before step j-1's output is
- * complete, as when x_j is computed from y_{j-1}; weights of later steps may
- * stream earlier (the gemv2 engine's prefetch of the next matrix,
- * board/kv260gemv/gemv2_dev.h:40-44). Each step equals w4a8_gemv_f32 on its
- * own, byte for byte. 1 <= n <= W4A8_CHAIN_MAX_STEPS. */
+ * Step j reads its activation only after every row of step j-1's output is
+ * written, so x_j may be (or be computed from) an earlier y; each step
+ * equals w4a8_gemv_f32 on its own, byte for byte. 1 <= n <=
+ * W4A8_CHAIN_MAX_STEPS.
+ *
+ * By default (W4A8_CHAIN_PER_STEP) each step is one kernel, in stream order.
+ * In W4A8_CHAIN_ONE_LAUNCH mode, a chain whose every k is in 2048..8192 is
+ * one cooperative launch instead: a workgroup per CU whose fetch waves
+ * stream the weights of the following matrices into LDS while its MAC
+ * waves compute the current one (the gemv2 engine's fetch / MAC split and
+ * the caller's prefetch of the next matrix, board/kv260gemv/gemv2_dev.h:
+ * 40-44, board/tp/tp_llama.cpp:364-368), with a grid barrier between steps.
+ * On MI355X that barrier, the activation staging it exposes and the skew
+ * between workgroups cost more per step than a kernel boundary, so the
+ * one-launch form is the slower one for the Llama-3.2-1B chain (its LM head
+ * alone is faster, its weights streamed during the last layer). One-launch
+ * chains on one device share that device's barrier state: they must not
+ * run concurrently (one stream per device, as the reference's single
+ * in-flight engine call), and the first one on a device allocates the state
+ * (64 KB), so it must not be inside a stream capture (such a call runs per
+ * step instead). */
 int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream);
+
+/* How w4a8_chain_gemv runs, for every later call in this process:
+ * W4A8_CHAIN_PER_STEP (the default) or W4A8_CHAIN_ONE_LAUNCH. */
+#define W4A8_CHAIN_ONE_LAUNCH 0
+#define W4A8_CHAIN_PER_STEP 1
+int w4a8_chain_set_mode(int mode);
+
+/* The one-launch chain's waits are bounded: a workgroup that polls the
+ * barrier this many times (~0.5 us each; default 4,194,304) gives up, every
+ * workgroup then skips the rest of the launch (its outputs are not valid)
+ * and the last one out restores the barrier state. w4a8_chain_timeouts
+ * returns how many launches on the current device gave up since its last
+ * call and clears the count (synchronous: waits for the device); it is 0
+ * whenever every launch completed. A limit <= 0 restores the default. */
+int w4a8_chain_set_spin_limit(int polls);
+int w4a8_chain_timeouts(void);
 
 /* The same n GEMVs with no order between them, in one launch: every matrix
  * streams at once, so small matrices no longer pay a launch and a latency

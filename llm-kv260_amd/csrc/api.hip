@@ -95,7 +95,7 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
 int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, float eps, float *act, int rows,
                            int k, void *stream) {
     if (int s = check_gemv(w, x, act, rows, k, 16)) return s;
-    if (k < 2048 || k > 8192 || rows % 2 || (rows / 2) % (64 / (k / 256))) return W4A8_ERR_SHAPE;
+    if (gate_up_silu_waves(rows, k) == 0) return W4A8_ERR_SHAPE;
     if (norm_w && !aligned(norm_w, 16)) return W4A8_ERR_ALIGN;
     XAux aux;
     aux.norm_w = norm_w;
@@ -213,6 +213,23 @@ int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream) {
     for (int i = 0; i < n; ++i)
         if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
     return hip_status(launch_chain(steps, n, (hipStream_t)stream));
+}
+
+int w4a8_chain_set_mode(int mode) {
+    if (mode != W4A8_CHAIN_ONE_LAUNCH && mode != W4A8_CHAIN_PER_STEP) return W4A8_ERR_SHAPE;
+    chain_set_mode(mode);
+    return W4A8_OK;
+}
+
+int w4a8_chain_set_spin_limit(int polls) {
+    chain_set_spin_limit(polls);
+    return W4A8_OK;
+}
+
+int w4a8_chain_timeouts(void) {
+    int n = 0;
+    if (int s = hip_status(chain_take_timeouts(&n))) return s;
+    return n;
 }
 
 int w4a8_gemv_batch(const w4a8_chain_step *steps, int n, void *stream) {

@@ -42,6 +42,7 @@
 
 #include "../../include/w4a8.h"
 #include "kernels.h"
+#include "gemv_tile.h"
 #include "q4_0_device.h"
 
 namespace w4a8 {
@@ -50,22 +51,6 @@ namespace {
 
 constexpr int MAX_THREADS = 512;
 constexpr size_t LDS_BUDGET = 160 * 1024;   // per CU on gfx950
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer accesses: the buffer unit range-checks every lane against the
-// resource's size, so a lane whose offset is out of range touches no memory
-// (a load returns zeros, a store is dropped). Loads and stores are then
-// issued by every lane on every path -- the number of memory operations a
-// wave has in flight never depends on data, and each wait is exact -- while
-// the lanes with nothing to do cost no traffic.
-constexpr int OUT_OF_RANGE = 0x7ffffff0;
-constexpr uint32_t BUFFER_DWORD3 = 0x00020000;   // raw dword access on gfx9-family parts
-constexpr int CACHE_NT = 2;                       // non-temporal (streamed once)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, BUFFER_DWORD3);
-}
 
 struct GemvParams {
     const uint8_t *seg[4];
@@ -158,172 +143,6 @@ __device__ __forceinline__ const uint8_t *chunk_ptr(const GemvParams &P, int r, 
     }
 }
 
-// Raw activation block as the global loads deliver it, before staging.
-template <int XF>
-struct XRaw;
-template <>
-struct XRaw<X_ENGINE> {
-    u32x4 q0, q1;
-    float d;
-};
-template <>
-struct XRaw<X_Q8_0> {
-    uint16_t h[17];
-};
-template <>
-struct XRaw<X_F32> {
-    float4 v[8];
-};
-template <>
-struct XRaw<X_RMS> {
-    float4 v[8];   // x
-    float4 w[8];   // norm weight
-};
-template <>
-struct XRaw<X_SILU> {
-    float4 g[8];   // gate
-    float4 u[8];   // up
-};
-
-__device__ __forceinline__ void load_f32_block(__amdgpu_buffer_rsrc_t rb, int off, float4 v[8]) {
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rb, off == OUT_OF_RANGE ? OUT_OF_RANGE : off + 16 * m, 0, 0);
-        v[m] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
-    }
-}
-
-// Block b of the activation; a lane with live == false reads nothing.
-template <int XF>
-__device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, XRaw<XF> &r,
-                                       const float *norm_w = nullptr) {
-    if constexpr (XF == X_RMS) {
-        load_f32_block(buffer_of(x, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.v);
-        load_f32_block(buffer_of(norm_w, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.w);
-    } else if constexpr (XF == X_SILU) {
-        const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(8 * k));
-        load_f32_block(xb, live ? 128 * b : OUT_OF_RANGE, r.g);
-        load_f32_block(xb, live ? 4 * k + 128 * b : OUT_OF_RANGE, r.u);
-    } else if constexpr (XF == X_ENGINE) {
-        const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(k + k / 8));
-        const int q_off = live ? 32 * b : OUT_OF_RANGE, d_off = live ? k + 4 * b : OUT_OF_RANGE;
-        r.q0 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off, 0, 0);
-        r.q1 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off + 16, 0, 0);
-        r.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xb, d_off, 0, 0));
-    } else if constexpr (XF == X_Q8_0) {
-        const uint16_t *src = reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(x) +
-                                                                 Q8_0_BYTES * (live ? b : 0));
-#pragma unroll
-        for (int i = 0; i < 17; ++i) r.h[i] = src[i];
-    } else {
-        const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(4 * k));
-        const int off = live ? 128 * b : OUT_OF_RANGE;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xb, off + 16 * m, 0, 0);
-            r.v[m] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
-        }
-    }
-}
-
-// The staged activation in LDS, one column per eight blocks (a chunk's
-// width): 64 dwords of activation nibbles (x_nibbles of block j of the column
-// at dword 8 j), the eight fp32 scales, the eight int32 corrections
-// -8 * sum(x), then 4 dwords of padding, 84 dwords in all. Lane l of a wave reads column l % C, so the lanes of one
-// LDS pass read eight different columns: at a stride of 84 dwords their
-// 16-byte reads fall on distinct banks, where a stride of 64 sent all of them
-// to the same ones (8-way conflicts at K = 2048, 32-way at K = 8192).
-constexpr int XCOL_DWORDS = 84;
-constexpr int XCOL_D = 64;     // the scales' offset in a column
-constexpr int XCOL_S = 72;     // the corrections'
-__host__ __device__ constexpr size_t x_lds_bytes(int nb) { return (size_t)(nb / 8) * XCOL_DWORDS * 4; }
-
-// Quantize (if fp32) and store block b into LDS: its values as nibbles, its
-// fp32 scale, and -8 times the sum of its int8 values.
-template <int XF>
-__device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_x, float rms_scale = 0.0f) {
-    uint32_t q[8];
-    float dx;
-    if constexpr (XF == X_ENGINE) {
-        q[0] = r.q0.x; q[1] = r.q0.y; q[2] = r.q0.z; q[3] = r.q0.w;
-        q[4] = r.q1.x; q[5] = r.q1.y; q[6] = r.q1.z; q[7] = r.q1.w;
-        dx = r.d;
-    } else if constexpr (XF == X_Q8_0) {
-        dx = half_bits_to_float(r.h[0]);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) q[m] = (uint32_t)r.h[1 + 2 * m] | ((uint32_t)r.h[2 + 2 * m] << 16);
-    } else {
-        float v[32];
-        if constexpr (XF == X_F32) {
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                v[4 * m] = r.v[m].x; v[4 * m + 1] = r.v[m].y; v[4 * m + 2] = r.v[m].z; v[4 * m + 3] = r.v[m].w;
-            }
-        } else if constexpr (XF == X_RMS) {
-            // out = (x * scale) * w, rmsnorm's last step (tp_llama.cpp:568).
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                const float xv[4] = {r.v[m].x, r.v[m].y, r.v[m].z, r.v[m].w};
-                const float wv[4] = {r.w[m].x, r.w[m].y, r.w[m].z, r.w[m].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float a = xv[e] * rms_scale;
-                    v[4 * m + e] = a * wv[e];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                const float gv[4] = {r.g[m].x, r.g[m].y, r.g[m].z, r.g[m].w};
-                const float uv[4] = {r.u[m].x, r.u[m].y, r.u[m].z, r.u[m].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[4 * m + e] = silu_mul(gv[e], uv[e]);
-            }
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
-        const float d = q8_scale(amax);
-        const float inv = safe_recip(d);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w |= ((uint32_t)(uint8_t)q8_round(v[4 * m + e], inv)) << (8 * e);
-            q[m] = w;
-        }
-        dx = half_bits_to_float(float_to_half_bits(d));
-    }
-    int32_t sum = 0;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) sum = __builtin_amdgcn_sdot4((int)q[m], 0x01010101, sum, false);
-    uint32_t xn[8];
-    x_nibbles(q, xn);
-    uint32_t *col = s_x + (b >> 3) * XCOL_DWORDS;
-    const int j = b & 7;
-    u32x4 *dst = reinterpret_cast<u32x4 *>(col + 8 * j);
-    dst[0] = (u32x4){xn[0], xn[1], xn[2], xn[3]};
-    dst[1] = (u32x4){xn[4], xn[5], xn[6], xn[7]};
-    col[XCOL_D + j] = __float_as_uint(dx);
-    col[XCOL_S + j] = (uint32_t)(-8 * sum);
-}
-
-// The eight terms of one chunk.
-__device__ __forceinline__ void chunk_terms(const uint32_t w[CHUNK_DWORDS], const uint32_t xv[8][8], const float xd[8],
-                                            const int32_t xs[8], float t[8]) {
-#define W4A8_TERM(J)                                                             \
-    {                                                                            \
-        uint32_t d_bits, qs[4];                                                  \
-        chunk_block<J>(w, d_bits, qs);                                           \
-        const int32_t sumi = block_dot_nib(qs, xv[J], xs[J]);                    \
-        t[J] = block_term(sumi, d_bits, xd[J]);                                  \
-    }
-    W4A8_TERM(0) W4A8_TERM(1) W4A8_TERM(2) W4A8_TERM(3)
-    W4A8_TERM(4) W4A8_TERM(5) W4A8_TERM(6) W4A8_TERM(7)
-#undef W4A8_TERM
-}
-
-constexpr int TILE_BYTES = 64 * CHUNK_BYTES;   // 9,216
 // Argmax workspace: the ticket counter and the merged key, each in its own 64-byte line.
 constexpr size_t ARGMAX_KEY_OFFSET = 64;
 // Tiles per wave held in registers. Two: a third (tried for plain matrices)
@@ -364,25 +183,10 @@ __device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lan
     }
 }
 
-__device__ __forceinline__ void wave_sync_lds() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // LDS layout (dynamic): per-wave slabs [waves][9216] | the staged activation
 // (nb / 8 columns of XCOL_DWORDS) | for X_RMS the float64 squares of x (33 per
 // block) and the scale. `block` / `nblocks` are this workgroup's index and the
 // number of workgroups sharing the matrix.
-// Raw buffer store of one fp32 to y[row]; a lane whose offset is past the end
-// of y stores nothing (the buffer unit drops out-of-range writes). Every lane
-// issues the instruction, so the number of memory operations a wave has in
-// flight never depends on data, and the waits for the prefetched tiles stay
-// exact.
-__device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t y, int byte_off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y, byte_off, 0, 0);
-}
-
 // ONE_PASS: a tile holds at most eight rows (K >= 2048), so one pass of the
 // ordered sums covers it and each lane stores at most one value per tile.
 // The workgroup's best key (its waves' keys through LDS) goes into the
@@ -562,43 +366,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         wave_sync_lds();
         // Accumulator a of row r: term a of chunks 0 .. C-1, in order, from
         // +0.0f. Eight rows per pass (more than one pass only when C < 8).
-        // The reads go eight at a time; a column past C contributes +0.0f,
-        // which leaves the sum unchanged (it started at +0.0f, so it is never
-        // -0.0f, and x + 0 = x for every other x).
-        auto lane_sum = [&](int r) {
-            float acc = 0.0f;
-            if (r < rpw) {
-                const float *src = s_t + r * C * 9 + acc_a;
-                if ((C & 7) == 0) {
-                    // Whole groups of eight (K a multiple of 2048): no guards,
-                    // and each group's reads go out before the previous
-                    // group's adds. The adds keep the chunk order.
-                    float v[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = src[9 * j];
-                    for (int c0 = 8; c0 < C; c0 += 8) {
-                        float nv[8];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) nv[j] = src[9 * (c0 + j)];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) acc = acc + v[j];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) v[j] = nv[j];
-                    }
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) acc = acc + v[j];
-                } else {
-                    for (int c0 = 0; c0 < C; c0 += 8) {
-                        float v[8];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) v[j] = c0 + j < C ? src[9 * (c0 + j)] : 0.0f;
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) acc = acc + v[j];
-                    }
-                }
-            }
-            return acc;
-        };
+        auto lane_sum = [&](int r) { return ordered_lane_sum(s_t, r, rpw, C, acc_a); };
         if constexpr (PAIR) {
             // Both halves issue one store; the gate's goes out of range.
             const float yv = tree8_dpp(lane_sum(acc_r));
@@ -872,26 +640,33 @@ hipError_t launch_batch_pass(const BatchParams &B, int max_k, hipStream_t stream
     return hipGetLastError();
 }
 
+// Waves per workgroup of the gate|up + silu launch: the grid has exactly
+// tiles / 2 waves (a wave's second tile is its first + tiles / 2), so the
+// workgroup size must divide tiles / 2 and hold one thread per activation
+// block; 0 when no size does (or the shape is outside 2048 <= k <= 8192,
+// whole tiles in each half).
+int gate_up_silu_waves(int rows, int k) {
+    if (k % 256 || k < 2048 || k > 8192 || rows < 2 || rows % 2) return 0;
+    const int rpw = 64 / (k / 256);
+    if ((rows / 2) % rpw) return 0;   // tiles may not straddle the two halves
+    const int half = rows / 2 / rpw;
+    const int nb = k / QK;
+    const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;
+    for (int wv = 4; wv >= min_waves && wv >= 1; wv >>= 1)
+        if (half % wv == 0) return wv;
+    return 0;
+}
+
 hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, float *act, int rows, int k,
                                     hipStream_t stream, XAux aux) {
-    if ((xf != X_F32 && xf != X_RMS) || k % 256 || k < 2048 || k > 8192 || rows < 2 || rows % 2) return hipErrorInvalidValue;
+    const int waves = gate_up_silu_waves(rows, k);
+    if ((xf != X_F32 && xf != X_RMS) || waves == 0) return hipErrorInvalidValue;
     GemvParams P{};
     derive_plain(P, w, x, act, rows, k);
     P.norm_w = aux.norm_w;
     P.eps = aux.eps;
-    // Tiles may not straddle the two halves.
-    if ((rows / 2) % P.rpw) return hipErrorInvalidValue;
     const int half = P.tiles / 2;
     const int nb = k / QK;
-    const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;
-    // The grid has exactly `half` waves, so that a wave's second tile is its first + half.
-    int waves = 0;
-    for (int wv = 4; wv >= min_waves && wv >= 1; wv >>= 1)
-        if (half % wv == 0) {
-            waves = wv;
-            break;
-        }
-    if (waves == 0) return hipErrorInvalidValue;
     const int grid = half / waves;
     const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? (size_t)(k + k / 32) * 8 + 16 : 0);
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
@@ -922,6 +697,12 @@ hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t st
 }
 
 hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream) {
+    if (chain_one_launch_fits(steps, n)) {
+        const hipError_t e = launch_chain_one(steps, n, stream);
+        // Too few CUs free for every workgroup to be resident: per step below.
+        if (e != hipErrorCooperativeLaunchTooLarge) return e;
+        (void)hipGetLastError();
+    }
     // One fused quantize + GEMV kernel per step; stream order carries the
     // step-to-step dependency.
     for (int i = 0; i < n; ++i) {

@@ -99,20 +99,26 @@ bool skip_value(Reader &r, uint32_t t, int depth) {
     return true;
 }
 
-// Data bytes of a tensor of a type the engine uses; 0 for other types.
+// Data bytes of a tensor of a type the engine uses, 0 for other types, and
+// UINT64_MAX when a used type's element or byte count overflows 64 bits (no
+// file holds that many bytes, so the range check refuses the tensor).
 uint64_t tensor_bytes(uint32_t type, const uint64_t ne[4]) {
-    uint64_t n = 1;
-    for (int d = 0; d < 4; ++d) {
-        if (ne[d] && n > UINT64_MAX / ne[d]) return 0;
-        n *= ne[d];
-    }
+    uint64_t per = 0, unit = 1;   // bytes per `unit` elements
     switch (type) {
-        case W4A8_GGML_TYPE_F32: return n * 4;
-        case W4A8_GGML_TYPE_F16: return n * 2;
-        case W4A8_GGML_TYPE_Q4_0: return ne[0] % 32 ? 0 : n / 32 * 18;
-        case W4A8_GGML_TYPE_Q8_0: return ne[0] % 32 ? 0 : n / 32 * 34;
+        case W4A8_GGML_TYPE_F32: per = 4; break;
+        case W4A8_GGML_TYPE_F16: per = 2; break;
+        case W4A8_GGML_TYPE_Q4_0: per = 18, unit = 32; break;
+        case W4A8_GGML_TYPE_Q8_0: per = 34, unit = 32; break;
         default: return 0;
     }
+    if (ne[0] % unit) return 0;
+    uint64_t n = 1;
+    for (int d = 0; d < 4; ++d) {
+        if (ne[d] && n > UINT64_MAX / ne[d]) return UINT64_MAX;
+        n *= ne[d];
+    }
+    n /= unit;
+    return n > UINT64_MAX / per ? UINT64_MAX : n * per;
 }
 
 }  // namespace

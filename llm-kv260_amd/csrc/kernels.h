@@ -86,8 +86,20 @@ struct w4a8_chain_step;   // include/w4a8.h
 
 namespace w4a8 {
 
-// The decode chain: one GEMV per step, in order, x quantized inside.
+// The decode chain: one GEMV per step, in order, x quantized inside. One
+// launch per step, or, in the one-launch mode when chain_one_launch_fits
+// (every k in 2048 .. 8192), one cooperative launch for the whole chain.
 hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream);
+bool chain_one_launch_fits(const w4a8_chain_step *steps, int n);
+hipError_t launch_chain_one(const w4a8_chain_step *steps, int n, hipStream_t stream);
+// The one-launch chain's bounded waits: polls before a wait gives up
+// (<= 0 restores the default), and the count of launches on the current
+// device that gave up since the last call (read and cleared; synchronous).
+void chain_set_spin_limit(int polls);
+hipError_t chain_take_timeouts(int *out);
+// 0: one launch when the chain fits; 1: one launch per step (the default).
+void chain_set_mode(int mode);
+int chain_mode();
 
 // The same GEMVs with no order between them, in one launch.
 hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream);
@@ -95,6 +107,8 @@ hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t st
 // x as X_F32 or X_RMS (aux), 2048 <= k <= 8192, n a multiple of 64 / (k / 256).
 hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, float *act, int rows, int k,
                                     hipStream_t stream, XAux aux = XAux{});
+// Its workgroup size in waves for a shape, 0 when the shape does not fit.
+int gate_up_silu_waves(int rows, int k);
 
 // w: float32[rows][K] -> Q4_0 rows.
 hipError_t launch_quantize_q4_0(const float *w, int rows, int k, uint8_t *out, hipStream_t stream);

@@ -25,6 +25,8 @@ Q4_0_BYTES = 18
 Q8_0_BYTES = 34
 LANES = 8
 MAX_K = 16384
+CHAIN_ONE_LAUNCH = 0
+CHAIN_PER_STEP = 1
 CONTRACT_VERSION = "llm-kv260/w4a8-q4_0-v2"
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -40,6 +42,7 @@ EXPORTS = (
     "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
     "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
     "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk", "w4a8_gemv_gate_up_silu",
+    "w4a8_chain_set_mode", "w4a8_chain_set_spin_limit", "w4a8_chain_timeouts",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -123,6 +126,11 @@ def lib() -> ctypes.CDLL:
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
         getattr(L, f).argtypes = [p, i, p]
         getattr(L, f).restype = i
+    for f in ("w4a8_chain_set_mode", "w4a8_chain_set_spin_limit"):
+        getattr(L, f).argtypes = [i]
+        getattr(L, f).restype = i
+    L.w4a8_chain_timeouts.argtypes = []
+    L.w4a8_chain_timeouts.restype = i
     _lib = L
     return L
 
@@ -164,6 +172,35 @@ def _need(t, dtype, name):
         raise ValueError(f"{name} must be contiguous")
 
 
+def _out(out, shape, dtype, like, name="out"):
+    """The caller's output tensor, checked before anything is launched (dtype,
+    device, contiguity and at least the elements the call writes), or a new
+    one. The C ABI sees only its address, so a short tensor would be written
+    past its end."""
+    import torch
+    numel = 1
+    for s in shape:
+        numel *= s
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=like.device)
+    if not isinstance(out, torch.Tensor):
+        raise TypeError(f"{name} must be a torch tensor, got {type(out).__name__}")
+    if out.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {out.dtype}")
+    if not out.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if out.numel() < numel:
+        raise ValueError(f"{name} holds {out.numel()} elements, the call writes {numel}")
+    if not out.is_cuda or out.device != like.device:
+        raise ValueError(f"{name} must be on {like.device}, got {out.device}")
+    return out
+
+
+def _same_device(t, like, name):
+    if t.device != like.device:
+        raise ValueError(f"{name} is on {t.device}, the weights on {like.device}")
+
+
 def _check_k(k: int) -> None:
     if k % 256 or not 256 <= k <= MAX_K:
         raise ValueError(f"K={k}: the engine needs K % 256 == 0 and 256 <= K <= {MAX_K}")
@@ -191,8 +228,7 @@ def quantize_q8_0_engine(x, out=None):
     _check_k(k)
     m = 1 if x.dim() == 1 else x.shape[0]
     shape = (engine_x_bytes(k),) if x.dim() == 1 else (m, engine_x_bytes(k))
-    if out is None:
-        out = torch.empty(shape, dtype=torch.uint8, device=x.device)
+    out = _out(out, shape, torch.uint8, x)
     check("w4a8_quantize_q8_0", lib().w4a8_quantize_q8_0(x.data_ptr(), out.data_ptr(), k, m, _stream(x)))
     return out
 
@@ -255,8 +291,9 @@ def gemv_engine(blocks, k: int, x_engine, out=None):
     _need(x_engine, torch.uint8, "x")
     if x_engine.numel() != engine_x_bytes(k):
         raise ValueError(f"engine x must be {engine_x_bytes(k)} bytes, got {x_engine.numel()}")
+    _same_device(x_engine, blocks, "x")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     check("w4a8_gemv", lib().w4a8_gemv(blocks.data_ptr(), x_engine.data_ptr(), y.data_ptr(), n, k,
                                        _stream(blocks)))
     return y
@@ -280,8 +317,9 @@ def gemv_q4_0_f32(blocks, k: int, x, out=None):
     _check_blocks(blocks, k)
     if tuple(x.shape) != (k,):
         raise ValueError(f"x must be [{k}], got {tuple(x.shape)}")
+    _same_device(x, blocks, "x")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     check("w4a8_gemv_f32", lib().w4a8_gemv_f32(blocks.data_ptr(), x.data_ptr(), y.data_ptr(), n, k,
                                                _stream(blocks)))
     return y
@@ -302,10 +340,16 @@ def gemv_gate_up_silu(blocks, k: int, x, norm_w=None, eps: float = 1e-5, out=Non
     _check_blocks(blocks, k)
     if tuple(x.shape) != (k,):
         raise ValueError(f"x must be [{k}], got {tuple(x.shape)}")
+    _same_device(x, blocks, "x")
     rows = blocks.shape[0]
-    act = torch.empty(rows // 2, dtype=torch.float32, device=blocks.device) if out is None else out
+    if rows % 2:
+        raise ValueError(f"gate|up needs an even number of rows (gate rows, then up rows), got {rows}")
     if norm_w is not None:
         _need(norm_w, torch.float32, "norm_w")
+        if tuple(norm_w.shape) != (k,):
+            raise ValueError(f"norm_w must be [{k}], got {tuple(norm_w.shape)}")
+        _same_device(norm_w, blocks, "norm_w")
+    act = _out(out, (rows // 2,), torch.float32, blocks)
     check("w4a8_gemv_gate_up_silu", lib().w4a8_gemv_gate_up_silu(
         blocks.data_ptr(), x.data_ptr(), None if norm_w is None else norm_w.data_ptr(), float(eps), act.data_ptr(),
         rows, k, _stream(blocks)))
@@ -340,8 +384,11 @@ def gemv_q4_0_f32_argmax(blocks, k: int, x, workspace, out=None):
     _check_blocks(blocks, k)
     if tuple(x.shape) != (k,):
         raise ValueError(f"x must be [{k}], got {tuple(x.shape)}")
+    _same_device(x, blocks, "x")
+    _need(workspace, torch.uint8, "workspace")
+    _same_device(workspace, blocks, "workspace")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     best = torch.empty(1, dtype=torch.int32, device=blocks.device)
     check("w4a8_gemv_f32_argmax", lib().w4a8_gemv_f32_argmax(
         blocks.data_ptr(), x.data_ptr(), y.data_ptr(), n, k, best.data_ptr(), workspace.data_ptr(),
@@ -357,8 +404,10 @@ def gemv_rmsnorm(blocks, k: int, x, norm_w, eps: float, out=None):
     _check_blocks(blocks, k)
     if tuple(x.shape) != (k,) or tuple(norm_w.shape) != (k,):
         raise ValueError(f"x and norm_w must be [{k}]")
+    _same_device(x, blocks, "x")
+    _same_device(norm_w, blocks, "norm_w")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     check("w4a8_gemv_rmsnorm", lib().w4a8_gemv_rmsnorm(blocks.data_ptr(), x.data_ptr(), norm_w.data_ptr(), eps,
                                                        y.data_ptr(), n, k, _stream(blocks)))
     return y
@@ -370,8 +419,14 @@ def gemv_rmsnorm_argmax(blocks, k: int, x, norm_w, eps: float, workspace, out=No
     _need(x, torch.float32, "x")
     _need(norm_w, torch.float32, "norm_w")
     _check_blocks(blocks, k)
+    if tuple(x.shape) != (k,) or tuple(norm_w.shape) != (k,):
+        raise ValueError(f"x and norm_w must be [{k}]")
+    _same_device(x, blocks, "x")
+    _same_device(norm_w, blocks, "norm_w")
+    _need(workspace, torch.uint8, "workspace")
+    _same_device(workspace, blocks, "workspace")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     best = torch.empty(1, dtype=torch.int32, device=blocks.device)
     check("w4a8_gemv_rmsnorm_argmax", lib().w4a8_gemv_rmsnorm_argmax(
         blocks.data_ptr(), x.data_ptr(), norm_w.data_ptr(), eps, y.data_ptr(), n, k, best.data_ptr(),
@@ -386,8 +441,9 @@ def gemv_silu_mul(blocks, k: int, gate_up, out=None):
     _check_blocks(blocks, k)
     if tuple(gate_up.shape) != (2 * k,):
         raise ValueError(f"gate_up must be [{2 * k}]")
+    _same_device(gate_up, blocks, "gate_up")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     check("w4a8_gemv_silu_mul", lib().w4a8_gemv_silu_mul(blocks.data_ptr(), gate_up.data_ptr(), y.data_ptr(), n, k,
                                                          _stream(blocks)))
     return y
@@ -398,7 +454,13 @@ def rmsnorm_q8_0_engine(x, norm_w, eps: float):
     import torch
     _need(x, torch.float32, "x")
     _need(norm_w, torch.float32, "norm_w")
+    if x.dim() not in (1, 2):
+        raise ValueError(f"x must be [k] or [m, k], got {tuple(x.shape)}")
     k = x.shape[-1]
+    _check_k(k)
+    if tuple(norm_w.shape) != (k,):
+        raise ValueError(f"norm_w must be [{k}], got {tuple(norm_w.shape)}")
+    _same_device(norm_w, x, "norm_w")
     m = 1 if x.dim() == 1 else x.shape[0]
     out = torch.empty((m, k + k // 8), dtype=torch.uint8, device=x.device)
     check("w4a8_rmsnorm_q8_0", lib().w4a8_rmsnorm_q8_0(x.data_ptr(), norm_w.data_ptr(), eps, out.data_ptr(), k, m,
@@ -410,7 +472,10 @@ def silu_mul_q8_0_engine(gate_up):
     """Engine-layout rows of Q8_0(silu(gate) * up) for gate_up float32 [2k] or [m, 2k]."""
     import torch
     _need(gate_up, torch.float32, "gate_up")
+    if gate_up.dim() not in (1, 2) or gate_up.shape[-1] % 2:
+        raise ValueError(f"gate_up must be [2k] or [m, 2k], got {tuple(gate_up.shape)}")
     k = gate_up.shape[-1] // 2
+    _check_k(k)
     m = 1 if gate_up.dim() == 1 else gate_up.shape[0]
     out = torch.empty((m, k + k // 8), dtype=torch.uint8, device=gate_up.device)
     check("w4a8_silu_mul_q8_0", lib().w4a8_silu_mul_q8_0(gate_up.data_ptr(), out.data_ptr(), k, m, _stream(gate_up)))
@@ -424,8 +489,9 @@ def gemv_q8_0_blocks(blocks, k: int, x_blocks, out=None):
     _need(x_blocks, torch.uint8, "x_blocks")
     if x_blocks.numel() != k // QK * Q8_0_BYTES:
         raise ValueError(f"Q8_0 x must be {k // QK * Q8_0_BYTES} bytes")
+    _same_device(x_blocks, blocks, "x_blocks")
     n = blocks.shape[0]
-    y = torch.empty(n, dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (n,), torch.float32, blocks)
     check("w4a8_gemv_q8_0", lib().w4a8_gemv_q8_0(blocks.data_ptr(), x_blocks.data_ptr(), y.data_ptr(), n, k,
                                                  _stream(blocks)))
     return y
@@ -436,9 +502,19 @@ def gemv_quarters(quarters, k: int, x_engine, rows: int, out=None):
     import torch
     if len(quarters) != 4:
         raise ValueError("need four quarters")
+    _check_k(k)
+    if rows < 4 or rows % 4:
+        raise ValueError(f"rows must be a positive multiple of 4, got {rows}")
+    _need(x_engine, torch.uint8, "x")
+    if x_engine.numel() != engine_x_bytes(k):
+        raise ValueError(f"engine x must be {engine_x_bytes(k)} bytes, got {x_engine.numel()}")
+    quarter_bytes = rows // 4 * q4_0_row_bytes(k)
     for q in quarters:
         _need(q, torch.uint8, "quarter")
-    y = torch.empty(rows, dtype=torch.float32, device=x_engine.device) if out is None else out
+        _same_device(q, x_engine, "quarter")
+        if q.numel() < quarter_bytes:
+            raise ValueError(f"a quarter holds {q.numel()} bytes, {rows // 4} rows need {quarter_bytes}")
+    y = _out(out, (rows,), torch.float32, x_engine)
     arr = (ctypes.c_void_p * 4)(*[q.data_ptr() for q in quarters])
     check("w4a8_gemv_quarters", lib().w4a8_gemv_quarters(arr, x_engine.data_ptr(), y.data_ptr(), rows, k,
                                                          _stream(x_engine)))
@@ -452,8 +528,9 @@ def gemm_engine(blocks, k: int, x_rows, out=None):
     _need(x_rows, torch.uint8, "x_rows")
     if x_rows.dim() != 2 or x_rows.shape[1] != engine_x_bytes(k):
         raise ValueError(f"x_rows must be [M, {engine_x_bytes(k)}], got {tuple(x_rows.shape)}")
+    _same_device(x_rows, blocks, "x_rows")
     m, n = x_rows.shape[0], blocks.shape[0]
-    y = torch.empty((m, n), dtype=torch.float32, device=blocks.device) if out is None else out
+    y = _out(out, (m, n), torch.float32, blocks)
     check("w4a8_gemm", lib().w4a8_gemm(blocks.data_ptr(), x_rows.data_ptr(), y.data_ptr(), m, n, k,
                                        _stream(blocks)))
     return y

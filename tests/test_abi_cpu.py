@@ -143,3 +143,50 @@ def test_shim_open_without_gpu_fails_cleanly():
     env = dict(os.environ, HIP_VISIBLE_DEVICES="-1", ROCR_VISIBLE_DEVICES="-1")
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
     assert r.stdout.split() == ["-1", "-1"], (r.stdout, r.stderr)
+
+
+# ------------------------------------------------- output tensors (Python)
+
+def test_out_tensor_checks_before_any_launch():
+    """The wrappers' check of a caller's out= tensor (kv260gemv._out): type,
+    dtype, contiguity and size are refused before anything is launched, and a
+    tensor off the weights' device too (here: any CPU tensor)."""
+    import torch
+    like = torch.empty(4, dtype=torch.uint8)
+    with pytest.raises(TypeError, match="torch tensor"):
+        kv260gemv._out(np.zeros(8, np.float32), (8,), torch.float32, like)
+    with pytest.raises(TypeError, match="float32"):
+        kv260gemv._out(torch.empty(8, dtype=torch.float16), (8,), torch.float32, like)
+    with pytest.raises(ValueError, match="contiguous"):
+        kv260gemv._out(torch.empty(16, dtype=torch.float32)[::2], (8,), torch.float32, like)
+    with pytest.raises(ValueError, match="holds 7 elements, the call writes 8"):
+        kv260gemv._out(torch.empty(7, dtype=torch.float32), (8,), torch.float32, like)
+    with pytest.raises(ValueError, match="holds 11 elements, the call writes 12"):
+        kv260gemv._out(torch.empty((3, 4), dtype=torch.float32)[:, :4].reshape(-1)[:11], (3, 4), torch.float32, like)
+    with pytest.raises(ValueError, match="must be on"):
+        kv260gemv._out(torch.empty(8, dtype=torch.float32), (8,), torch.float32, like)
+
+
+def test_wrappers_refuse_host_tensors():
+    """Every wrapper refuses CPU tensors with a TypeError / ValueError before it
+    calls the library (no GPU here: a call would fail with a HIP error)."""
+    import torch
+    k = 256
+    blocks = torch.zeros((16, k // 32 * 18), dtype=torch.uint8)
+    x = torch.zeros(k, dtype=torch.float32)
+    calls = [
+        lambda: kv260gemv.gemv_q4_0_f32(blocks, k, x),
+        lambda: kv260gemv.gemv_engine(blocks, k, torch.zeros(k + k // 8, dtype=torch.uint8)),
+        lambda: kv260gemv.gemv_rmsnorm(blocks, k, x, x, 1e-5),
+        lambda: kv260gemv.gemv_silu_mul(blocks, k, torch.zeros(2 * k)),
+        lambda: kv260gemv.gemv_q8_0_blocks(blocks, k, torch.zeros(k // 32 * 34, dtype=torch.uint8)),
+        lambda: kv260gemv.gemm_engine(blocks, k, torch.zeros((2, k + k // 8), dtype=torch.uint8)),
+        lambda: kv260gemv.quantize_q8_0_engine(x),
+        lambda: kv260gemv.rmsnorm_q8_0_engine(x, x, 1e-5),
+        lambda: kv260gemv.silu_mul_q8_0_engine(torch.zeros(2 * k)),
+        lambda: kv260gemv.gemv_quarters([blocks] * 4, k, torch.zeros(k + k // 8, dtype=torch.uint8), 64),
+        lambda: kv260gemv.topk(x, 4),
+    ]
+    for c in calls:
+        with pytest.raises((TypeError, ValueError)):
+            c()

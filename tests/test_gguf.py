@@ -151,3 +151,18 @@ def test_mutated_files_open_or_are_refused(tmp_path):
             assert e.status == -6
             refused += 1
     assert opened and refused
+
+
+@pytest.mark.parametrize("gtype,ne0", [(GGML_TYPE_F32, (1 << 62) + 32), (GGML_TYPE_F16, (1 << 63) + 32),
+                                       (GGML_TYPE_Q4_0, 1 << 63), (GGML_TYPE_F32, (1 << 61) + 64)])
+def test_byte_count_overflow_is_refused(tmp_path, gtype, ne0):
+    """A tensor whose element count fits 64 bits but whose byte count does not
+    (2^62 + 32 float32 values are 2^64 + 128 bytes, 128 modulo 2^64) must not
+    pass the range check with a wrapped-around size: the file is refused."""
+    data = b"\0" * 256
+    blob, *_ = gguf_bytes([("general.architecture", STRING, "llama")], [("big", gtype, (ne0,), data)])
+    path = tmp_path / "big.gguf"
+    path.write_bytes(blob)
+    with pytest.raises(W4A8Error) as e:
+        GGUFFile(path)
+    assert e.value.status == -6

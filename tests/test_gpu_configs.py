@@ -144,6 +144,35 @@ def test_config3_decode_chain_400_steps(gpu):
     check("batch")
 
 
+def test_config3_one_launch_chain(gpu):
+    """The 65-matrix chain as one cooperative launch (W4A8_CHAIN_ONE_LAUNCH):
+    byte-exact after the first launch and after 50 more, no wait given up."""
+    import torch
+    chain, recs = cf.decode_chain(), FIX["config3"]
+    mats, xs, ys = [], [], []
+    for m in chain:
+        mats.append(device_blocks(gpu, m))
+        xs.append(dev(cf.activation(m)))
+        ys.append(poisoned_f32(m.rows))
+    steps = step_array(mats, xs, ys, [(m.rows, m.k) for m in chain])
+    ptr = ctypes.cast(steps, ctypes.c_void_p)
+    L = gpu.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert L.w4a8_chain_set_mode(0) == 0
+    try:
+        assert L.w4a8_chain_timeouts() >= 0
+        for launches, what in ((1, "first launch"), (50, "after 51 launches")):
+            for y in ys:
+                y.fill_(float("nan"))
+            for _ in range(launches):
+                gpu.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, len(chain), stream))
+            for m, y, rec in zip(chain, ys, recs):
+                assert sha(host(y)) == rec["y"], f"{what}: {m.name}"
+        assert L.w4a8_chain_timeouts() == 0
+    finally:
+        L.w4a8_chain_set_mode(1)
+
+
 def test_config4_m_sweep(gpu):
     """M = 1 .. 64 activation rows through the int8-MFMA path, each row byte-exact."""
     recs = {(r["name"], r["m"]): r for r in FIX["config4"]}

@@ -137,5 +137,8 @@ def test_gemv_gate_up_silu_rejects(gpu):
     assert call(63, 2048) == -2        # odd rows
     assert call(12, 2048) == -2        # n = 6 is not a multiple of 8 rows per tile
     assert call(64, 1024) == -2        # k below 2048
+    assert call(4, 8192) == -2         # one tile per half at k = 8192: not a multiple of 4
+    assert call(8, 4096) == -2         # one tile per half at k = 4096: not a multiple of 2
+    assert call(12, 8192) == -2        # three tiles per half at k = 8192
     assert call(64, 2048) == 0
     torch.cuda.synchronize()
