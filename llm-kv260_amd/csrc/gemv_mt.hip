@@ -1,0 +1,279 @@
+// W4A8 GEMV for a few tokens at once (2 <= m <= 8): Y[t][n] = W[n, K] x_t for
+// m engine-layout activation rows, each output byte-identical to the M = 1
+// GEMV on that row alone (the contract takes one x at a time,
+// src/llm_kv260/q4_0.py:164-165).
+//
+// At small m the work is still the weight stream: m = 8 adds 0.4% to the
+// bytes of an 8,192-column matrix. So this is the M = 1 kernel's streaming
+// (gemv_m1.hip) with the arithmetic repeated per token, not a contraction on
+// MFMA, whose 16-token tiles would be mostly padding here:
+//  * Each wave streams 9,216-byte tiles of whole rows with nine coalesced
+//    16-byte raw buffer loads per lane, two tiles in flight, through a per-wave
+//    LDS slab, so that lane l holds chunk l (eight consecutive blocks of a
+//    row, 144 bytes).
+//  * A lane pulls its eight blocks' fp16 scales and packed nibbles out of the
+//    chunk once, with the nibble sums that v_dot8_u32_u4's form of the block
+//    dot needs (block_dot_nib, q4_0_device.h), and keeps them for every token.
+//  * Per token it reads its chunk column of that token's staged activation
+//    (LDS, one copy per token, the layout x_stage writes) and computes the
+//    eight terms (f32(sumi) * d_w) * d_x, then the contract's ordered lane
+//    sums and adjacent-pair tree through the slab, exactly as for M = 1.
+// The activation rows are staged once per workgroup, their loads issued
+// before the first weight tile's so that the staging waits for them only.
+#include <atomic>
+
+#include "../../include/w4a8.h"
+#include "gemv_tile.h"
+#include "kernels.h"
+#include "q4_0_device.h"
+
+namespace w4a8 {
+
+namespace {
+
+constexpr int MT_MAX = 8;                        // tokens per launch
+constexpr int MT_THREADS = 512;
+constexpr size_t MT_LDS_BUDGET = 160 * 1024;
+
+struct MtParams {
+    const uint8_t *w;
+    const uint8_t *x;      // m rows of the engine layout, x_stride bytes apart
+    float *y;              // y[m][rows]
+    int m, rows, k, C, rpw, tiles, x_stride;
+};
+
+struct MtTile {
+    u32x4 p[CHUNK_PIECES];
+};
+
+// Tile `tile` of the matrix (lane l: bytes 1024 p + 16 l of it); a tile past
+// the end reads nothing, and the last tile's bytes past the matrix read zeros.
+__device__ __forceinline__ void mt_load_tile(const MtParams &P, int tile, int lane, MtTile &t) {
+    const size_t tile_bytes = (size_t)P.rpw * (size_t)P.C * CHUNK_BYTES;
+    const size_t total = (size_t)P.rows * (size_t)P.C * CHUNK_BYTES;
+    const size_t off0 = (size_t)__builtin_amdgcn_readfirstlane(tile) * tile_bytes;
+    const bool in = off0 < total;
+    const uint32_t n = in ? (uint32_t)(total - off0 < (size_t)TILE_BYTES ? total - off0 : (size_t)TILE_BYTES) : 0u;
+    const __amdgpu_buffer_rsrc_t tb = buffer_of(P.w + (in ? off0 : 0), n);
+#pragma unroll
+    for (int p = 0; p < CHUNK_PIECES; ++p) t.p[p] = __builtin_amdgcn_raw_buffer_load_b128(tb, 1024 * p + 16 * lane, 0, CACHE_NT);
+}
+
+// sum(n) of one block's 32 unsigned nibbles: the token-independent term of
+// block_dot_nib, computed once per block and kept for every token.
+__device__ __forceinline__ uint32_t nibble_sum(const uint32_t qs[4]) {
+    uint32_t n = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) n = __builtin_amdgcn_udot8(qs[k], 0x11111111u, n, false);
+    return n;
+}
+
+// block_dot_nib with sum(n) given: the same terms, so the same int32.
+__device__ __forceinline__ int32_t block_dot_with_sum(const uint32_t qs[4], uint32_t n, const uint32_t xn[8],
+                                                      int32_t c8) {
+    uint32_t a = 0, b = (uint32_t)c8;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        a = __builtin_amdgcn_udot8(qs[k], xn[k], a, false);
+        b = __builtin_amdgcn_udot8(qs[k], xn[4 + k], b, false);
+    }
+    return (int32_t)(16u * a + b) - 128 * (int32_t)n;
+}
+
+// PASSES: staging rounds of blocks per thread, m * nb <= PASSES * threads.
+// TG: tokens computed per round of ordered sums.
+template <int PASSES, int TG>
+__device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t *lds) {
+    const int nb = P.k >> 5;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nthreads = blockDim.x, waves = nthreads >> 6;
+    uint8_t *slab = lds + (size_t)wave * TILE_BYTES;
+    uint32_t *s_x = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
+    const int tok_dwords = (int)(x_lds_bytes(nb) / 4);
+
+    const int C = P.C, rpw = P.rpw;
+    const int my_r = lane / C, my_c = lane - my_r * C;
+    const int colx = my_r < rpw ? my_c : 0;
+
+    // 1. The activation rows' loads, before any weight tile's.
+    XRaw<X_ENGINE> xr[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int i = tid + p * nthreads;
+        const int t = i / nb, b = i - t * nb;
+        const bool live = t < P.m;
+        x_load<X_ENGINE>(P.x + (size_t)(live ? t : 0) * P.x_stride, P.k, b, live, xr[p]);
+    }
+
+    int tile = block * waves + wave;
+    const int tstride = nblocks * waves;
+    const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
+
+    auto stage_x = [&]() {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int i = tid + p * nthreads;
+            const int t = i / nb, b = i - t * nb;
+            if (t < P.m) x_stage<X_ENGINE>(xr[p], b, s_x + t * tok_dwords);
+        }
+        __syncthreads();
+    };
+
+    const int acc_r = lane >> 3, acc_a = lane & 7;
+    const __amdgpu_buffer_rsrc_t y_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * P.rows * P.m, BUFFER_DWORD3);
+
+    // One tile: buffer -> slab -> chunk -> blocks; then per token: terms ->
+    // slab -> ordered lane sums -> tree -> y[t][row]. With refill the buffer
+    // then receives the tile two strides ahead.
+    auto step = [&](MtTile &bt, bool refill) {
+        u32x4 *wslab = reinterpret_cast<u32x4 *>(slab);
+#pragma unroll
+        for (int p = 0; p < CHUNK_PIECES; ++p) wslab[64 * p + lane] = bt.p[p];
+        wave_sync_lds();
+        uint32_t w[CHUNK_DWORDS];
+        {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(slab + CHUNK_BYTES * lane);
+#pragma unroll
+            for (int q = 0; q < CHUNK_PIECES; ++q) {
+                const u32x4 v = src[q];
+                w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+            }
+        }
+        if (refill) mt_load_tile(P, tile + 2 * tstride, lane, bt);
+        uint32_t qs[8][4], dw[8], ns[8];
+#define W4A8_BLK(J)                           \
+    chunk_block<J>(w, dw[J], qs[J]);          \
+    ns[J] = nibble_sum(qs[J]);
+        W4A8_BLK(0) W4A8_BLK(1) W4A8_BLK(2) W4A8_BLK(3) W4A8_BLK(4) W4A8_BLK(5) W4A8_BLK(6) W4A8_BLK(7)
+#undef W4A8_BLK
+        float *s_t = reinterpret_cast<float *>(slab);
+        const int row = tile * rpw + acc_r;
+        const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
+        // Tokens in groups of TG (2 or 4): their terms take TG x 64 lanes x 9
+        // floats of the slab (all of it at TG = 4), so each group takes one
+        // pair of syncs.
+        for (int t0 = 0; t0 < P.m; t0 += TG) {
+            float term[TG][8];
+#pragma unroll
+            for (int u = 0; u < TG; ++u) {
+                const int t = t0 + u < P.m ? t0 + u : t0;   // past m: t0 again, never stored
+                const uint32_t *col = s_x + t * tok_dwords + colx * XCOL_DWORDS;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const u32x4 *src = reinterpret_cast<const u32x4 *>(col + 8 * j);
+                    const u32x4 a = src[0], c = src[1];
+                    const uint32_t xn[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+                    const int32_t sumi = block_dot_with_sum(qs[j], ns[j], xn, (int32_t)col[XCOL_S + j]);
+                    term[u][j] = block_term(sumi, dw[j], __uint_as_float(col[XCOL_D + j]));
+                }
+            }
+            wave_sync_lds();
+#pragma unroll
+            for (int u = 0; u < TG; ++u)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s_t[u * 576 + 9 * lane + j] = term[u][j];
+            wave_sync_lds();
+#pragma unroll
+            for (int u = 0; u < TG; ++u) {
+                const float yv = tree8_dpp(ordered_lane_sum(s_t + u * 576, acc_r, rpw, C, acc_a));
+                const bool store = mine && t0 + u < P.m;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), y_rsrc,
+                                                      store ? 4 * ((t0 + u) * P.rows + row) : OUT_OF_RANGE, 0, 0);
+            }
+        }
+        wave_sync_lds();
+        tile += tstride;
+    };
+
+    // 2. Straight-line paths per wave (no tile, one tile, or the two-deep
+    // pipeline), so that every wait on the loads in flight is exact.
+    if (n_my >= 2) {
+        MtTile buf[2];
+        mt_load_tile(P, tile, lane, buf[0]);
+        mt_load_tile(P, tile + tstride, lane, buf[1]);
+        stage_x();
+        int done = 0;
+        for (; done + 2 <= n_my; done += 2) {
+            step(buf[0], true);
+            step(buf[1], true);
+        }
+        if (done < n_my) step(buf[0], false);
+    } else if (n_my == 1) {
+        MtTile b;
+        mt_load_tile(P, tile, lane, b);
+        stage_x();
+        step(b, false);
+    } else {
+        stage_x();
+    }
+}
+
+template <int PASSES, int TG>
+__global__ __launch_bounds__(MT_THREADS) void gemv_mt_kernel(MtParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    gemv_mt_body<PASSES, TG>(P, blockIdx.x, gridDim.x, lds);
+}
+
+template <int PASSES>
+hipError_t launch_mt_pass(const MtParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
+    auto go = [&](const void *fn, auto kernel) {
+        const hipError_t e = allow_dynamic_lds(fn, MT_LDS_BUDGET);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), lds, stream, P);
+        return hipGetLastError();
+    };
+    if (P.m <= 2) return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 2>), gemv_mt_kernel<PASSES, 2>);
+    return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 4>), gemv_mt_kernel<PASSES, 4>);
+}
+
+}  // namespace
+
+bool gemv_mt_fits(int m, int rows, int k) {
+    return m >= 2 && m <= MT_MAX && k >= 2048 && k <= 8192 && k % 256 == 0 &&
+           (size_t)rows * (size_t)(k / QK * Q4_0_BYTES) < 0x7fff0000u && (size_t)m * rows * 4 < 0x7fff0000u;
+}
+
+hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, int rows, int k, hipStream_t stream) {
+    if (!gemv_mt_fits(m, rows, k)) return hipErrorInvalidValue;
+    MtParams P{};
+    P.w = w;
+    P.x = x;
+    P.y = y;
+    P.m = m;
+    P.rows = rows;
+    P.k = k;
+    P.C = k / 256;
+    P.rpw = 64 / P.C;
+    P.tiles = (rows + P.rpw - 1) / P.rpw;
+    P.x_stride = k + k / 8;
+    const int nb = k / QK;
+    const int cus = device_cu_count();
+    // Launch shapes as for M = 1 (gemv_m1.hip), with workgroups of at least
+    // four waves, so that the m activation rows are staged by enough threads:
+    //  * up to eight tiles per CU (every layer matrix): one workgroup per CU
+    //    at most, one tile per wave, every tile in flight at once;
+    //  * more (the LM head): four-wave workgroups striding over the matrix,
+    //    two per CU.
+    int waves, grid;
+    if (P.tiles <= 8 * cus) {
+        const int per_cu = (P.tiles + cus - 1) / cus;
+        waves = per_cu < 4 ? 4 : per_cu;
+        grid = (P.tiles + waves - 1) / waves;
+    } else {
+        waves = 4;
+        grid = (P.tiles + waves - 1) / waves;
+        if (grid > 2 * cus) grid = 2 * cus;
+    }
+    const int threads = 64 * waves;
+    const int passes = (m * nb + threads - 1) / threads;
+    const size_t lds = (size_t)waves * TILE_BYTES + (size_t)m * x_lds_bytes(nb);
+    if (lds > MT_LDS_BUDGET) return hipErrorInvalidValue;
+    if (passes <= 1) return launch_mt_pass<1>(P, grid, threads, lds, stream);
+    if (passes <= 2) return launch_mt_pass<2>(P, grid, threads, lds, stream);
+    if (passes <= 4) return launch_mt_pass<4>(P, grid, threads, lds, stream);
+    return launch_mt_pass<8>(P, grid, threads, lds, stream);
+}
+
+}  // namespace w4a8

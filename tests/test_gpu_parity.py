@@ -244,7 +244,11 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       (3, 8200, 512), (17, 8208, 1024), (40, 8240, 2048), (64, 8192, 512),
                                       (130, 8256, 1536),
                                       # the largest K, on both kernels
-                                      (40, 64, 16384), (5, 8200, 16384)])
+                                      (40, 64, 16384), (5, 8200, 16384),
+                                      # the few-token GEMV (m = 2, or m <= 4 on large matrices):
+                                      # ragged rows, one row, 48-chunk tiles (k = 6144), k = 8192
+                                      (2, 1, 4096), (2, 300, 6144), (3, 8200, 2048), (4, 8197, 2048),
+                                      (4, 2048, 8192), (3, 1000, 8192), (2, 5, 8192)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
@@ -257,7 +261,8 @@ def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     assert_bytes_equal(host(y), want, "gemm")
 
 
-@pytest.mark.parametrize("m,rows,k", [(24, 8200, 1024), (40, 2000, 1024)])
+@pytest.mark.parametrize("m,rows,k", [(24, 8200, 1024), (40, 2000, 1024), (2, 2000, 2048), (4, 8200, 2048),
+                                      (3, 600, 8192)])
 def test_gemm_random_bytes(gpu, m, rows, k):
     """Arbitrary block bytes and activations (any finite fp16 scale) through both M > 1
     kernels (8,200 rows: the row-split one), row by row against the contract."""
