@@ -1,6 +1,7 @@
 """Benchmark of the MI355X W4A8 engine on the Llama-3.2-1B decode GEMV chain.
 
     python bench.py [--gpus 1] [--steps 400] [--warmup 20] [--no-cpu] [--no-gemv]
+                    [--no-caller] [--chain-only]
 
 One step = one token's 65 W4A8 GEMVs (16 x q|k|v 3072x2048, o 2048x2048,
 gate|up 16384x2048, down 2048x8192, then the LM head 128256x2048), each
@@ -11,11 +12,23 @@ captured once into a HIP graph and replayed. Weights (695,107,584 bytes of
 Q4_0) are resident in HBM; the chain alone is larger than the 256 MB Infinity
 Cache, so every step streams from HBM.
 
+The chain runs on configuration 3's seeded inputs (weights default_rng(1000 +
+j), activations default_rng(2000 + j)). The outputs are poisoned after the
+warm-up, and after the timed replays every byte of all 65 outputs is compared
+(SHA-256) with the oracle's digests in tests/golden/configs.json; the line
+says "verified": true only when they all match. The GEMM sweep (configuration
+4) and the 24-token prefill are checked the same way.
+
 Prints one JSON line. Besides the chain (value), it reports:
   roofline     the chain's kernel (the fused quantize + GEMV, 65 launches per
                step): average algorithmic bytes per launch / average launch
                duration, both over the timed region (HIP events on the launch
-               stream around the graph replays)
+               stream around the graph replays, launch boundaries included);
+               beside it, kernel_durations: the same bytes over the sum of the
+               65 kernels' average durations in the committed rocprofv3 trace
+               of `bench.py --chain-only`
+  chain_one_launch  the chain as one cooperative launch per step
+               (W4A8_CHAIN_ONE_LAUNCH), verified the same way
   batch        the same 65 GEMVs per step in one w4a8_gemv_batch launch (no
                order inside a step)
   gemv         microseconds per GEMV at every shape, weights rotated past the
@@ -32,6 +45,10 @@ Prints one JSON line. Besides the chain (value), it reports:
                headers: llm-kv260_amd/caller/engine_caller) on both engines:
                host-visible ms per token and us per call, split into the
                host quantize, the clean / invalidate copies and start + wait
+  calls        what one call costs (llm-kv260_amd/caller/call_costs), column
+               for column against the reference's per-call table: the
+               synchronous gemv_dev_run, the device-side time per call, the
+               standalone Q8_0 quantize, the clean / invalidate copies
   cpu_baseline the NumPy restatement of the contract on one core, and the
                C restatement on all cores, over one decode step
 All launches come from C through the library's ABI; Python only sets them up.
@@ -80,7 +97,7 @@ class CStep(ctypes.Structure):
 
 def device_weights(torch, kv, rows, k, seed):
     """Q4_0 blocks of an N(0, 0.02) fp32 matrix drawn with the device RNG and
-    quantized by the engine's own Q4_0 kernel."""
+    quantized by the engine's own Q4_0 kernel (timing-only shapes)."""
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     w = torch.randn((rows, k), generator=g, device="cuda", dtype=torch.float32) * 0.02
@@ -89,19 +106,69 @@ def device_weights(torch, kv, rows, k, seed):
     return blocks
 
 
+FIXTURES = os.path.join(ROOT, "tests", "golden", "configs.json")
+
+
+def fixtures():
+    with open(FIXTURES) as f:
+        return json.load(f)
+
+
+def sha(a) -> str:
+    import hashlib
+    import numpy as np
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def host_weights(cf, m):
+    """fp32 weights of one configuration matrix, drawn on the host from its seed."""
+    import numpy as np
+    w = np.empty((m.rows, m.k), np.float32)
+    for r0, part in cf.weight_chunks(m):
+        w[r0:r0 + part.shape[0]] = part
+    return w
+
+
+def seeded_blocks(torch, kv, cf, matrices):
+    """Q4_0 blocks of the configuration matrices' seeded weights, drawn on the
+    host (numpy releases the GIL, so eight threads draw at once) and quantized
+    on the GPU by the engine's Q4_0 kernel."""
+    from concurrent.futures import ThreadPoolExecutor
+    out = []
+    with ThreadPoolExecutor(8) as pool:
+        for i, w in enumerate(pool.map(lambda m: host_weights(cf, m), matrices)):
+            out.append(kv.quantize_q4_0(torch.from_numpy(w).cuda()))
+            del w
+            if i % 16 == 15:
+                log(f"seeded weights: {i + 1}/{len(matrices)} matrices")
+    torch.cuda.synchronize()
+    return out
+
+
+def verify(pairs) -> dict:
+    """pairs: (name, device tensor, expected sha256). Every byte of every output."""
+    bad = [name for name, t, want in pairs if sha(t.cpu().numpy()) != want]
+    return {"ok": not bad, "outputs": len(pairs), "mismatched": bad[:8]}
+
+
 def build_chain(torch, kv, cf):
+    """Config 3: the 65 matrices' seeded weights and activations, whose outputs
+    tests/golden/configs.json holds the oracle's digests of."""
     chain = cf.decode_chain()
-    mats, xs, ys = [], [], []
-    for i, m in enumerate(chain):
-        mats.append(device_weights(torch, kv, m.rows, m.k, m.w_seed))
-        xs.append(torch.from_numpy(cf.activation(m)).cuda())
-        ys.append(torch.empty(m.rows, dtype=torch.float32, device="cuda"))
-        if i % 16 == 15:
-            log(f"chain weights: {i + 1}/{len(chain)} matrices")
+    recs = fixtures()["config3"]
+    mats = seeded_blocks(torch, kv, cf, chain)
+    weights_ok = all(sha(b.cpu().numpy()) == r["q4_0"] for b, r in zip(mats, recs))
+    xs = [torch.from_numpy(cf.activation(m)).cuda() for m in chain]
+    ys = [torch.empty(m.rows, dtype=torch.float32, device="cuda") for m in chain]
     steps = (CStep * len(chain))(*[CStep(mats[i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), m.rows, m.k)
                                    for i, m in enumerate(chain)])
     torch.cuda.synchronize()
-    return chain, mats, xs, ys, steps
+    return chain, mats, xs, ys, steps, recs, weights_ok
+
+
+def poison(ts):
+    for t in ts:
+        t.fill_(float("nan"))
 
 
 def graph_of(torch, stream, calls):
@@ -118,12 +185,17 @@ def graph_of(torch, stream, calls):
     return g
 
 
-def time_replays(torch, stream, g, n, warmup):
-    """ms per replay over exactly n replays, synchronized on both sides."""
+def time_replays(torch, stream, g, n, warmup, before=None):
+    """ms per replay over exactly n replays, synchronized on both sides.
+    before(): run after the warm-up, outside the timed region (e.g. poison the
+    outputs so that what is verified afterwards was written by the timed replays)."""
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             g.replay()
     torch.cuda.synchronize()
+    if before is not None:
+        before()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
@@ -301,29 +373,32 @@ def time_prefill(torch, kv, cf, chain, mats, stream, mrows, reps=5):
     (int8 MFMA), in order, from a HIP graph. The reference prefills one decode
     pass per token (docs/buildlog/0008-openai-api.md:73-74)."""
     L = kv.lib()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(11)
-    calls, keep = [], []
+    calls, keep, ys = [], [], []
     for i, m in enumerate(chain):
-        x = torch.randn((mrows, m.k), generator=g, device="cuda")
+        x = torch.from_numpy(cf.prefill_activation(i, mrows, m.k)).cuda()
         xe = torch.empty((mrows, m.k + m.k // 8), dtype=torch.uint8, device="cuda")
         y = torch.empty((mrows, m.rows), dtype=torch.float32, device="cuda")
-        keep += [x, xe, y]
+        keep += [x, xe]
+        ys.append(y)
         calls.append((lambda w, x, xe, y, m: lambda s: kv.check("prefill", L.w4a8_quantize_q8_0(
             x.data_ptr(), xe.data_ptr(), m.k, mrows, s) or L.w4a8_gemm(w.data_ptr(), xe.data_ptr(), y.data_ptr(),
                                                                       mrows, m.rows, m.k, s)))(mats[i], x, xe, y, m))
     gr = graph_of(torch, stream, calls)
-    ms, _ = time_replays(torch, stream, gr, reps, 1)
-    del gr, keep
+    ms, _ = time_replays(torch, stream, gr, reps, 1, before=lambda: poison(ys))
+    recs = fixtures().get(f"config3_prefill{mrows}")
+    checked = verify([(r["name"], y, r["y"]) for y, r in zip(ys, recs)]) if recs else None
+    del gr, keep, ys
     torch.cuda.empty_cache()
     return {"tokens": mrows, "ms_per_prompt": round(ms, 4), "tokens_per_s": round(mrows / (ms * 1e-3), 1),
-            "launches": 2 * len(chain)}
+            "launches": 2 * len(chain), "verified": checked["ok"] if checked else None,
+            "verification": checked or "no digests for this prompt length (timing only)"}
 
 
-def time_gemm(torch, kv, cf, m, mrows, stream):
-    """us per M > 1 GEMM (engine-layout activation rows), rotating weight copies."""
+def time_gemm(torch, kv, cf, m, mrows, stream, base, rec):
+    """us per M > 1 GEMM (engine-layout activation rows) over rotating copies of
+    config 4's seeded weights `base`; the output of the timed launches is
+    checked against the oracle's digest `rec`."""
     L = kv.lib()
-    base = device_weights(torch, kv, m.rows, m.k, 8)
     copies = max(3, -(-ROTATE_BYTES // m.weight_bytes))
     mats = [base] + [base.clone() for _ in range(copies - 1)]
     xr = kv.quantize_q8_0_engine(torch.from_numpy(cf.gemm_activation(mrows, m.k)).cuda())
@@ -332,12 +407,13 @@ def time_gemm(torch, kv, cf, m, mrows, stream):
                                                                     mrows, m.rows, m.k, s))))(mats[i])
              for i in range(copies)]
     g = graph_of(torch, stream, calls)
-    ms, _ = time_replays(torch, stream, g, 5, 1)
+    ms, _ = time_replays(torch, stream, g, 5, 1, before=lambda: poison([y]))
+    ok = verify([(f"{m.name} M={mrows}", y, rec["y"])])["ok"]
     us = ms * 1e3 / copies
     nbytes = m.weight_bytes + mrows * (m.k + m.k // 8) + 4 * mrows * m.rows
-    del g, mats, base
+    del g, mats
     return {"shape": f"{m.rows}x{m.k}", "m": mrows, "us": round(us, 3), "gbps": round(nbytes / us / 1e3, 1),
-            "tops": round(2 * mrows * m.rows * m.k / us / 1e6, 2)}
+            "tops": round(2 * mrows * m.rows * m.k / us / 1e6, 2), "verified": ok}
 
 
 CALLER = os.path.join(ROOT, "llm-kv260_amd", "caller", "engine_caller")
@@ -356,6 +432,41 @@ def run_caller(tokens=20):
             raise RuntimeError(f"engine_caller {name} failed: {p.stderr[-500:]}")
         out[name] = json.loads(p.stdout.strip().splitlines()[-1])
     return out
+
+
+CALL_COSTS = os.path.join(ROOT, "llm-kv260_amd", "caller", "call_costs")
+
+
+def run_call_costs():
+    """Per-call costs through the reference ABI (the reference's bench_calls
+    table, docs/buildlog/evidence/0012-bench-calls.txt), in a process of its own."""
+    import subprocess
+    env = dict(os.environ, KV260GEMV_UDMABUF_SIZES="udmabuf0=512M")
+    p = subprocess.run([CALL_COSTS, "--reps", "200"], capture_output=True, text=True, timeout=300, env=env)
+    if p.returncode != 0:
+        raise RuntimeError(f"call_costs failed: {p.stderr[-500:]}")
+    out = json.loads(p.stdout.strip().splitlines()[-1])
+    out["reference_board"] = {"source": "docs/buildlog/evidence/0012-bench-calls.txt (KV260, one rank's shard)",
+                              "raw_best_us": {"tiny": 2.8, "x2048": 4.6, "x8192": 10.4},
+                              "q8_us": {"k256": {"ref": 3.8, "neon": 1.0}, "k2048": {"ref": 30.3, "neon": 8.3},
+                                        "k8192": {"ref": 121.7, "neon": 33.5}}}
+    return out
+
+
+KERNEL_SUMMARY = os.path.join("profiles", "gemv_kernels_llama1b_chain_only.txt")
+
+
+def kernel_durations():
+    """The chain's per-step sum of kernel durations from the committed rocprofv3
+    kernel trace of `bench.py --chain-only` (its JSON line), or None."""
+    try:
+        with open(os.path.join(ROOT, KERNEL_SUMMARY)) as f:
+            for line in f:
+                if line.startswith("JSON "):
+                    return json.loads(line[5:])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(chain, mats, xs, budget_s=30.0):
@@ -397,6 +508,65 @@ def cpu_baseline(chain, mats, xs, budget_s=30.0):
     }
 
 
+def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic):
+    """The fields every bench line carries: the metric, the chain and its roofline."""
+    n = len(cf.decode_chain())
+    chain_bytes = cf.chain_algorithmic_bytes()
+    kernel = None
+    if kd.get("per_step_sum_us"):
+        ks = kd["per_step_sum_us"]
+        kernel = {"source": KERNEL_SUMMARY, "sum_us_per_step": ks,
+                  "achieved": round(chain_bytes / (ks * 1e-6) / 1e9, 1),
+                  "frac": round(chain_bytes / (ks * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                  "profiled_run_us_per_step": kd.get("profiled_us_per_step"),
+                  "note": "the sum of the 65 kernels' average durations (rocprofv3 kernel trace of "
+                          "bench.py --chain-only): the time the chain's kernels run, without the launch "
+                          "boundaries between them"}
+    return {
+        "metric": "1B-shape decode GEMV-chain tokens/s (W4A8 Q4_0 x Q8_0, 65 GEMVs per token)",
+        "value": round(1e3 / ms_per_step, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xint8->int32, fp32 epilogue",
+        "data": "synthetic, seeded: config 3's Q4_0 weights (numpy default_rng(1000 + j) N(0, 0.02), quantized "
+                "on the GPU) and fp32 N(0, 1) activations (default_rng(2000 + j)); the timed outputs are "
+                "checked against the oracle's SHA-256 digests in tests/golden/configs.json",
+        "config": {"workload": "llama-3.2-1b decode GEMV chain: 16 x (qkv 3072x2048, o 2048x2048, "
+                               "gate_up 16384x2048, down 2048x8192) + lm_head 128256x2048, M=1, "
+                               "activation re-quantized to Q8_0 before every matrix, matrices in order",
+                   "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
+                   "algorithmic_bytes_per_step": chain_bytes},
+        "verified": (chain_check["ok"] and chain_check["weights_ok"] and
+                     (one_launch is None or one_launch["verified"])),
+        "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("chain_traffic_bytes_per_launch"), "traffic_source": PMC_SUMMARY,
+                     "kernel": "gemv_m1_kernel<X_F32> (fused Q8_0 quantize + GEMV), the chain's 65 launches",
+                     "bytes_per_launch": round(chain_bytes / n), "us_per_launch": round(ms_per_step * 1e3 / n, 3),
+                     "timing": "HIP events on the launch stream around the timed graph replays: step time / 65, "
+                               "launch boundaries included",
+                     "kernel_durations": kernel},
+        "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "gbps": round(chain_gbs, 1),
+                  "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4), "launches_per_step": n,
+                  "verified": chain_check["ok"], "verification": chain_check,
+                  "dependency": "matrix j+1 starts after matrix j's output is complete"},
+        "chain_one_launch": one_launch,
+        "wall_s_timed": round(wall, 3),
+    }
+
+
+def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd):
+    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, pmc_traffic() or {})
+    out["mode"] = "chain only" + ("" if one_launch is None else " (per-step chain, then the one-launch chain)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -404,7 +574,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the per-shape GEMV and GEMM timings")
-    ap.add_argument("--no-caller", action="store_true", help="skip the reference-ABI caller (a child process)")
+    ap.add_argument("--no-caller", action="store_true",
+                    help="skip the reference-ABI caller and the per-call costs (child processes)")
+    ap.add_argument("--chain-only", action="store_true",
+                    help="time the chain (per-step, then one launch per step) and stop: the run the "
+                         "chain's kernel-trace profile is taken from")
+    ap.add_argument("--no-one-launch", action="store_true",
+                    help="skip the one-launch (cooperative) chain")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first copy MB of device memory once: a plain copy of known size whose "
                          "FETCH_SIZE / WRITE_SIZE counters scale the kernels' HBM traffic")
@@ -430,28 +606,61 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"calibration copy: {args.copy_calibration} MB")
         del src, dst
-    log("building the 65-matrix decode chain on the device")
-    chain, mats, xs, ys, steps = build_chain(torch, kv, cf)
+    log("building the 65-matrix decode chain (config 3's seeded weights) on the device")
+    chain, mats, xs, ys, steps, recs, weights_ok = build_chain(torch, kv, cf)
     n = len(chain)
     chain_bytes = cf.chain_algorithmic_bytes()
     ptr = ctypes.cast(steps, ctypes.c_void_p)
+    chain_digests = [(r["name"], y, r["y"]) for y, r in zip(ys, recs)]
 
     log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay)")
     g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
-    ms_per_step, wall = time_replays(torch, stream, g_chain, args.steps, args.warmup)
+    ms_per_step, wall = time_replays(torch, stream, g_chain, args.steps, args.warmup, before=lambda: poison(ys))
+    chain_check = verify(chain_digests)
+    chain_check["weights_ok"] = weights_ok
     tok_s = 1e3 / ms_per_step
     chain_gbs = chain_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"chain: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s")
+    log(f"chain: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s, "
+        f"outputs {'match' if chain_check['ok'] else 'DIFFER FROM'} the oracle's digests")
+    del g_chain
 
-    g_batch = graph_of(torch, stream, [lambda s: kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, s))])
-    ms_batch, _ = time_replays(torch, stream, g_batch, args.steps, args.warmup)
-    batch_gbs = chain_bytes / (ms_batch * 1e-3) / 1e9
-    log(f"batch: {ms_batch * 1e3:.1f} us/step, {batch_gbs:.0f} GB/s (one launch, no order inside a step)")
-    del g_chain, g_batch
-    prefill = [time_prefill(torch, kv, cf, chain, mats, stream, mr) for mr in (24, 64)]
-    for r in prefill:
-        log(f"prefill {r['tokens']} tokens: {r['ms_per_prompt']} ms, {r['tokens_per_s']} tokens/s "
-            f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token)")
+    # The same chain as one cooperative launch per step (opt-in mode).
+    one_launch = None
+    if not args.no_one_launch:
+        assert L.w4a8_chain_set_mode(kv.CHAIN_ONE_LAUNCH) == 0
+        try:
+            timeouts0 = L.w4a8_chain_timeouts()
+            g_one = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
+            ms_one, _ = time_replays(torch, stream, g_one, args.steps, args.warmup, before=lambda: poison(ys))
+            one_check = verify(chain_digests)
+            one_check["waits_given_up"] = L.w4a8_chain_timeouts() - timeouts0
+            del g_one
+        finally:
+            L.w4a8_chain_set_mode(kv.CHAIN_PER_STEP)
+        one_launch = {"us_per_step": round(ms_one * 1e3, 2), "tokens_per_s": round(1e3 / ms_one, 1),
+                      "gbps": round(chain_bytes / (ms_one * 1e-3) / 1e9, 1), "launches_per_step": 1,
+                      "kernel": "chain_kernel (cooperative, grid barrier between matrices)",
+                      "verified": one_check["ok"] and one_check["waits_given_up"] == 0, "verification": one_check}
+        log(f"one-launch chain: {one_launch['us_per_step']} us/step, verified {one_launch['verified']}")
+
+    if not args.chain_only:
+        g_batch = graph_of(torch, stream, [lambda s: kv.check("w4a8_gemv_batch", L.w4a8_gemv_batch(ptr, n, s))])
+        ms_batch, _ = time_replays(torch, stream, g_batch, args.steps, args.warmup, before=lambda: poison(ys))
+        batch_check = verify(chain_digests)
+        batch_gbs = chain_bytes / (ms_batch * 1e-3) / 1e9
+        log(f"batch: {ms_batch * 1e3:.1f} us/step, {batch_gbs:.0f} GB/s (one launch, no order inside a step), "
+            f"verified {batch_check['ok']}")
+        del g_batch
+        prefill = [time_prefill(torch, kv, cf, chain, mats, stream, mr) for mr in (cf.PREFILL_M, 64)]
+        for r in prefill:
+            log(f"prefill {r['tokens']} tokens: {r['ms_per_prompt']} ms, {r['tokens_per_s']} tokens/s "
+                f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token), verified {r['verified']}")
+    kd = kernel_durations() or {}
+    if args.chain_only:
+        out = chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd)
+        print(json.dumps(out), flush=True)
+        return 0 if out["verified"] else 1
+
     fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup)
     staged = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, silu_epilogue=False)
     fused_chain["silu_in_down_staging_us_per_step"] = staged["us_per_step"]
@@ -467,11 +676,14 @@ def main() -> int:
         log(f"gemv {m.name} {r['shape']}: {r['us']} us, {r['gbps']} GB/s")
         torch.cuda.empty_cache()
     if not args.no_gemv:
-        for m in cf.GEMM_SHAPES:
+        g4 = {(r["name"], r["m"]): r for r in fixtures()["config4"]}
+        for m, base in zip(cf.GEMM_SHAPES, seeded_blocks(torch, kv, cf, cf.GEMM_SHAPES)):
             for mrows in cf.GEMM_M:
-                r = time_gemm(torch, kv, cf, m, mrows, stream)
+                r = time_gemm(torch, kv, cf, m, mrows, stream, base, g4[(m.name, mrows)])
                 gemm.append(dict(name=m.name, **r))
-                log(f"gemm {m.name} M={mrows}: {r['us']} us, {r['gbps']} GB/s, {r['tops']} TOP/s")
+                log(f"gemm {m.name} M={mrows}: {r['us']} us, {r['gbps']} GB/s, {r['tops']} TOP/s, "
+                    f"verified {r['verified']}")
+            del base
             torch.cuda.empty_cache()
     producers = {} if args.no_gemv else time_producers(torch, kv, cf, stream)
     for name, r in producers.items():
@@ -484,41 +696,30 @@ def main() -> int:
     lm_gbs = cf.LM_HEAD.algorithmic_bytes / lm["us"] / 1e3
 
     traffic = pmc_traffic() or {}
-    caller = None
+    caller = calls = None
     if not args.no_caller:
         log("the reference's caller through the reference ABI (host-visible)")
         caller = run_caller()
+        log("per-call costs through the reference ABI")
+        calls = run_call_costs()
     for name, r in (caller or {}).items():
         log(f"caller {name}: {r['ms_per_token']:.3f} ms/token, {r['us_per_call']['total']:.1f} us/call host-visible")
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
         cpu = cpu_baseline(chain, mats, xs)
+    verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and
+                (one_launch is None or one_launch["verified"]) and
+                all(r["verified"] for r in gemm) and prefill[0]["verified"] is True)
 
-    out = {
-        "metric": "1B-shape decode GEMV-chain tokens/s (W4A8 Q4_0 x Q8_0, 65 GEMVs per token)",
-        "value": round(tok_s, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int4xint8->int32, fp32 epilogue",
-        "data": "synthetic: Q4_0 weights from N(0,0.02) drawn with the device RNG per matrix and quantized by "
-                "the engine; fp32 N(0,1) activations, numpy-seeded per matrix",
-        "config": {"workload": "llama-3.2-1b decode GEMV chain: 16 x (qkv 3072x2048, o 2048x2048, "
-                               "gate_up 16384x2048, down 2048x8192) + lm_head 128256x2048, M=1, "
-                               "activation re-quantized to Q8_0 before every matrix, matrices in order",
-                   "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
-                   "algorithmic_bytes_per_step": chain_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("chain_traffic_bytes_per_launch"), "traffic_source": PMC_SUMMARY,
-                     "kernel": "gemv_m1_kernel<X_F32> (fused Q8_0 quantize + GEMV), the chain's 65 launches",
-                     "bytes_per_launch": round(chain_bytes / n), "us_per_launch": round(ms_per_step * 1e3 / n, 3)},
+    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic)
+    out["verified"] = verified
+    out["verification"] = {"chain": chain_check, "batch": batch_check,
+                           "one_launch": one_launch["verified"] if one_launch else None,
+                           "gemm": {f"{r['name']} M={r['m']}": r["verified"] for r in gemm},
+                           "prefill24": prefill[0]["verification"],
+                           "digests": "tests/golden/configs.json (config3, config3_prefill24, config4)"}
+    out.update({
         "roofline_batch": {"achieved": round(batch_gbs, 1), "frac": round(batch_gbs / HBM_PEAK_GBS, 4),
                            "unit": "GB/s", "kernel": "gemv_batch_kernel, one step's 65 GEMVs per launch",
                            "traffic": traffic.get("batch_traffic_bytes_per_launch"),
@@ -527,12 +728,9 @@ def main() -> int:
                              "kernel": "gemv_m1_kernel<X_ENGINE>, LM head 128256x2048, 3 rotating weight copies",
                              "traffic": traffic.get("lm_head_traffic_bytes_per_launch"),
                              "bytes_per_launch": cf.LM_HEAD.algorithmic_bytes, "us_per_launch": lm["us"]},
-        "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "gbps": round(chain_gbs, 1),
-                  "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4), "launches_per_step": n,
-                  "dependency": "matrix j+1 starts after matrix j's output is complete"},
         "batch": {"us_per_step": round(ms_batch * 1e3, 2), "gbps": round(batch_gbs, 1),
                   "hbm_frac": round(batch_gbs / HBM_PEAK_GBS, 4), "launches_per_step": 1,
-                  "tokens_per_s": round(1e3 / ms_batch, 1),
+                  "tokens_per_s": round(1e3 / ms_batch, 1), "verified": batch_check["ok"],
                   "dependency": "none inside a step (w4a8_gemv_batch); steps in order"},
         "gemv": gemv,
         "gemm": gemm,
@@ -541,9 +739,9 @@ def main() -> int:
         "chain_fused_producers": fused_chain,
         "prefill": prefill,
         "caller": caller,
+        "calls": calls,
         "cpu_baseline": cpu,
-        "wall_s_timed": round(wall, 3),
-    }
+    })
     print(json.dumps(out), flush=True)
     return 0
 

@@ -88,8 +88,12 @@ int w4a8_gemv_f32_argmax(const void *w, const float *x, float *y, int rows, int 
  * reference's insertion sort leaves them: values descending, among equal
  * values (-0 equal to +0) the smaller index first, and a value at or below
  * -1e30 never admitted; slots left over hold {-1e30, 0} as there. vals are
- * y's own values (bit for bit). A NaN logit is never a candidate (the
- * reference's handling of one depends on its position). Two launches
+ * y's own values (bit for bit). NaN logits are handled as the reference's
+ * loop handles them: a NaN takes the last slot (v <= NaN is false), evicting
+ * the k-th candidate held at that point, and the next logit then enters
+ * whatever its value, so a NaN can be a candidate and can cost one. When y
+ * holds a NaN the second launch runs that loop itself, in order, in one
+ * wave (slower: a sequential pass over y). Two launches
  * through `workspace`: w4a8_topk_workspace_bytes(n) bytes of device memory,
  * 8-byte aligned, overwritten by each call. 1 <= n <= 262144. */
 size_t w4a8_topk_workspace_bytes(int n);

@@ -1,0 +1,211 @@
+// What one engine call costs on the MI355X, column for column against the
+// reference's per-call table (board/kv260gemv/bench_calls.c, printed in
+// docs/buildlog/evidence/0012-bench-calls.txt):
+//
+//   raw       gemv_dev_run alone through the reference ABI (gemv_dev.h): the
+//             host-visible time of one synchronous call, best and mean of N
+//   clean     udmabuf_clean of x (k + k/8 bytes host -> device), best
+//   inval_y   udmabuf_invalidate of y (4 rows bytes device -> host), best
+//   graph     the device-side time per call: N w4a8_gemv launches captured in
+//             one HIP graph, replayed, HIP events around the replay, / N
+//             (the kernel plus the launch boundary, no host in the loop)
+//   q8        the standalone Q8_0 quantize of a float32 x (w4a8_quantize_q8_0,
+//             the reference's q8ref / q8neon columns run on the CPU): host-
+//             visible launch + stream sync, best and mean, and device-side
+//             per launch from a graph
+//
+// Shapes: the reference's tiny / x2048 / x8192 rows (16 output rows), then
+// the unsplit single-GPU shapes of the Llama-3.2-1B decode (one GPU holds
+// the whole model, so no shard of four). Weights are valid Q4_0 blocks with
+// seeded nibbles (timing does not depend on the values); the weights of one
+// shape are read from HBM on every call, each call on the same buffers as
+// in the reference's table.
+//
+// Usage: call_costs [--reps N]. Prints one JSON line.
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include <hip/hip_runtime_api.h>
+
+extern "C" {
+#include "gemv_dev.h"
+#include "udmabuf.h"
+#include "w4a8.h"
+}
+
+#define DIE(...)                                     \
+    do {                                             \
+        fprintf(stderr, "call_costs: " __VA_ARGS__); \
+        fprintf(stderr, "\n");                       \
+        exit(1);                                     \
+    } while (0)
+
+#define HIP_OK(e)                                                              \
+    do {                                                                       \
+        hipError_t err_ = (e);                                                 \
+        if (err_ != hipSuccess) DIE("%s: %s", #e, hipGetErrorString(err_));    \
+    } while (0)
+
+static double now() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec + ts.tv_nsec * 1e-9;
+}
+
+struct Stat {
+    double best = 1e30, sum = 0;
+    int n = 0;
+    void add(double s) {
+        best = std::min(best, s);
+        sum += s;
+        ++n;
+    }
+    double best_us() const { return best * 1e6; }
+    double mean_us() const { return n ? sum / n * 1e6 : 0; }
+};
+
+struct Shape {
+    const char *name;
+    int k, rows;
+};
+
+static uint64_t mix(uint64_t &s) {
+    s ^= s >> 12;
+    s ^= s << 25;
+    s ^= s >> 27;
+    return s * 0x2545F4914F6CDD1Dull;
+}
+
+int main(int argc, char **argv) {
+    int reps = 200;
+    for (int i = 1; i < argc; ++i) {
+        if (!strcmp(argv[i], "--reps") && i + 1 < argc) reps = atoi(argv[++i]);
+        else DIE("usage: call_costs [--reps N]");
+    }
+    if (reps < 1) DIE("--reps must be positive");
+    const Shape shapes[] = {{"tiny", 256, 16},      {"x2048", 2048, 16},       {"x8192", 8192, 16},
+                            {"qkv", 2048, 3072},    {"o", 2048, 2048},         {"gate_up", 2048, 16384},
+                            {"down", 8192, 2048},   {"lm_head", 2048, 128256}};
+
+    udmabuf_t pool;
+    if (udmabuf_open(&pool, "udmabuf0")) DIE("no pool udmabuf0 (KV260GEMV_UDMABUF_SIZES)");
+    gemv_dev_t dev;
+    if (gemv_dev_open(&dev)) DIE("gemv_q4_0 engine not available");
+    hipStream_t s;
+    HIP_OK(hipStreamCreate(&s));
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+
+    std::string out = "{\"reps\": " + std::to_string(reps) + ", \"shapes\": [";
+    uint64_t seed = 12345;
+    for (size_t si = 0; si < sizeof shapes / sizeof shapes[0]; ++si) {
+        const Shape &sh = shapes[si];
+        const size_t wbytes = (size_t)sh.rows * sh.k / 32 * 18, xbytes = sh.k + sh.k / 8, ybytes = 4ull * sh.rows;
+        pool.used = 0;
+        uint8_t *w = (uint8_t *)udmabuf_alloc(&pool, wbytes, 64 << 10);
+        uint8_t *x = (uint8_t *)udmabuf_alloc(&pool, xbytes + 64, 4096);
+        uint8_t *y = (uint8_t *)udmabuf_alloc(&pool, ybytes, 4096);
+        float *xf = (float *)udmabuf_alloc(&pool, 4ull * sh.k, 4096);
+        uint8_t *xq = (uint8_t *)udmabuf_alloc(&pool, xbytes, 4096);
+        if (!w || !x || !y || !xf || !xq) DIE("pool too small for %s", sh.name);
+        for (size_t b = 0; b < wbytes; b += 18) {          // scale 2^-10 (fp16 0x1400), seeded nibbles
+            w[b] = 0x00;
+            w[b + 1] = 0x14;
+            for (int j = 2; j < 18; ++j) w[b + j] = (uint8_t)mix(seed);
+        }
+        for (int i = 0; i < sh.k; ++i) x[i] = (uint8_t)(mix(seed) % 255 + 129);   // int8 in -127..127
+        for (int b = 0; b < sh.k / 32; ++b) {
+            const float d = 1.0f / 64;
+            memcpy(x + sh.k + 4 * b, &d, 4);
+        }
+        for (int i = 0; i < sh.k; ++i) xf[i] = (float)((int)(mix(seed) % 2001) - 1000) / 500.0f;
+        udmabuf_clean(w, wbytes);
+        udmabuf_clean(x, xbytes);
+        udmabuf_clean(xf, 4ull * sh.k);
+        const uint64_t wp = udmabuf_phys(&pool, w), xp = udmabuf_phys(&pool, x), yp = udmabuf_phys(&pool, y);
+        const uint64_t xfp = udmabuf_phys(&pool, xf), xqp = udmabuf_phys(&pool, xq);
+
+        // raw: one synchronous call through the reference ABI.
+        Stat raw, clean, inval, q8host;
+        for (int r = 0; r < 5; ++r) gemv_dev_run(&dev, wp, xp, yp, sh.k, sh.rows);
+        for (int r = 0; r < reps; ++r) {
+            const double a = now();
+            gemv_dev_run(&dev, wp, xp, yp, sh.k, sh.rows);
+            raw.add(now() - a);
+        }
+        for (int r = 0; r < reps; ++r) {
+            double a = now();
+            udmabuf_clean(x, xbytes);
+            clean.add(now() - a);
+            a = now();
+            udmabuf_invalidate(y, ybytes);
+            inval.add(now() - a);
+        }
+        // q8: the standalone quantize, launch + sync, host-visible.
+        for (int r = 0; r < 5; ++r)
+            if (w4a8_quantize_q8_0((const float *)xfp, (void *)xqp, sh.k, 1, s)) DIE("quantize %s", sh.name);
+        HIP_OK(hipStreamSynchronize(s));
+        for (int r = 0; r < reps; ++r) {
+            const double a = now();
+            w4a8_quantize_q8_0((const float *)xfp, (void *)xqp, sh.k, 1, s);
+            HIP_OK(hipStreamSynchronize(s));
+            q8host.add(now() - a);
+        }
+
+        // graph: device-side per call, for the GEMV and for the quantize.
+        auto graph_us = [&](bool quantize) {
+            const int n = 50;
+            hipGraph_t g;
+            hipGraphExec_t ge;
+            HIP_OK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            for (int i = 0; i < n; ++i) {
+                const int rc = quantize ? w4a8_quantize_q8_0((const float *)xfp, (void *)xqp, sh.k, 1, s)
+                                        : w4a8_gemv((const void *)wp, (const void *)xp, (float *)yp, sh.rows, sh.k, s);
+                if (rc) DIE("launch under capture (%s): %d", sh.name, rc);
+            }
+            HIP_OK(hipStreamEndCapture(s, &g));
+            HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+            const int replays = std::max(2, std::min(20, reps / 10));
+            HIP_OK(hipGraphLaunch(ge, s));
+            HIP_OK(hipStreamSynchronize(s));
+            HIP_OK(hipEventRecord(e0, s));
+            for (int i = 0; i < replays; ++i) HIP_OK(hipGraphLaunch(ge, s));
+            HIP_OK(hipEventRecord(e1, s));
+            HIP_OK(hipEventSynchronize(e1));
+            float ms = 0;
+            HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+            HIP_OK(hipGraphExecDestroy(ge));
+            HIP_OK(hipGraphDestroy(g));
+            return ms * 1e3 / (replays * n);
+        };
+        const double gemv_graph = graph_us(false), q8_graph = graph_us(true);
+
+        char buf[1024];
+        snprintf(buf, sizeof buf,
+                 "%s{\"shape\": \"%s\", \"k\": %d, \"rows\": %d, \"weight_mb\": %.3f, \"raw_best_us\": %.2f, "
+                 "\"raw_mean_us\": %.2f, \"raw_gbps\": %.2f, \"graph_us\": %.3f, \"clean_x_us\": %.2f, "
+                 "\"inval_y_us\": %.2f, \"q8_host_best_us\": %.2f, \"q8_host_mean_us\": %.2f, \"q8_graph_us\": %.3f}",
+                 si ? ", " : "", sh.name, sh.k, sh.rows, wbytes / 1e6, raw.best_us(), raw.mean_us(),
+                 wbytes / raw.best / 1e9, gemv_graph, clean.best_us(), inval.best_us(), q8host.best_us(),
+                 q8host.mean_us(), q8_graph);
+        out += buf;
+        fprintf(stderr, "call_costs: %-8s raw %.2f us (mean %.2f), graph %.3f us, q8 %.2f us host / %.3f us graph\n",
+                sh.name, raw.best_us(), raw.mean_us(), gemv_graph, q8host.best_us(), q8_graph);
+    }
+    out += "]}";
+    printf("%s\n", out.c_str());
+    HIP_OK(hipEventDestroy(e0));
+    HIP_OK(hipEventDestroy(e1));
+    HIP_OK(hipStreamDestroy(s));
+    gemv_dev_close(&dev);
+    udmabuf_close(&pool);
+    return 0;
+}

@@ -9,9 +9,8 @@
 // -0 taken as +0, which the reference's comparisons treat as equal) above
 // the complemented index, so that the largest key is the largest value and,
 // among equal values, the smallest index. A value that the reference would
-// never admit (v <= -1e30, and NaN, which this version excludes as well)
-// gets key 0. The k largest keys are then exactly the reference's k
-// candidates, in its order, for every input without NaN.
+// never admit (v <= -1e30) gets key 0. The k largest keys are then exactly
+// the reference's k candidates, in its order, for every input without NaN.
 //
 // Stage 1: one 256-thread workgroup per 1024 logits. Each wave holds 256
 // keys, four per lane as four lists of 64 (one key per lane each), sorts the
@@ -21,6 +20,16 @@
 // workgroup merges those lists pairwise, level by level. A merge of two
 // descending lists A and B keeps, in lane l, max(A[l], B[63 - l]): a bitonic
 // sequence holding their 64 best, which six compare-exchange steps sort.
+//
+// A NaN logit has no place in that order: the reference's loop admits it
+// (v <= NaN is false) into the last slot, evicting the k-th candidate it
+// held at that point, and then admits the next logit whatever its value,
+// so the result depends on where the NaN stands. A stage-1 workgroup that
+// sees a NaN marks its list (first key all ones, which no value's key can
+// be: NaN is the only float whose order bits are all ones), and stage 2,
+// finding a mark, runs the reference's loop itself, in order, in one wave
+// (topk_in_order): the same candidates, bit for bit, at the cost of one
+// pass over y by a single wave.
 #include "kernels.h"
 
 namespace w4a8 {
@@ -32,8 +41,10 @@ constexpr int TOPK_LIST = 64;         // candidates each list keeps (k <= 64)
 constexpr int TOPK_MAX_LISTS = 256;   // stage 2's LDS: 256 x 64 keys = 128 KB
 static_assert(TOPK_LIST == 64, "the index arithmetic below takes lists of 64");
 
+constexpr unsigned long long NAN_MARK = ~0ull;   // a stage-1 list whose slice holds a NaN
+
 __device__ __forceinline__ unsigned long long topk_key(float v, int i) {
-    if (!(v > -1e30f)) return 0ull;                                  // never admitted (and NaN)
+    if (!(v > -1e30f)) return 0ull;                                  // never admitted (NaN: see NAN_MARK)
     const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
     const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
@@ -105,22 +116,84 @@ __global__ __launch_bounds__(256) void topk_stage1(const float *__restrict__ y, 
         const int i = base + 64 * r + lane;
         k[r] = sort64(i < n ? topk_key(v[r], i) : 0ull, lane);
     }
+    bool nan = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) nan = nan || (base + 64 * r + lane < n && v[r] != v[r]);
     const unsigned long long m01 = merge64(k[0], __shfl(k[1], 63 - lane), lane);
     const unsigned long long m23 = merge64(k[2], __shfl(k[3], 63 - lane), lane);
     wl[wave][lane] = merge64(m01, __shfl(m23, 63 - lane), lane);
-    __syncthreads();
+    const bool slice_has_nan = __syncthreads_or(nan);
     if (wave == 0) {
         const unsigned long long a = merge64(wl[0][lane], wl[1][63 - lane], lane);
         const unsigned long long b = merge64(wl[2][lane], wl[3][63 - lane], lane);
-        lists[(size_t)blockIdx.x * TOPK_LIST + lane] = merge64(a, __shfl(b, 63 - lane), lane);
+        const unsigned long long best = merge64(a, __shfl(b, 63 - lane), lane);
+        lists[(size_t)blockIdx.x * TOPK_LIST + lane] = slice_has_nan && lane == 0 ? NAN_MARK : best;
     }
 }
 
-__global__ __launch_bounds__(1024) void topk_stage2(const float *__restrict__ y, const unsigned long long *lists,
-                                                    int nlists, int k, float *__restrict__ vals,
+// The reference's loop (tp_llama.cpp:902-908) as written, over y[0..n) in
+// order, in one wave: lane j holds slot j (value bits and index). A logit is
+// taken when !(v <= last slot's value); each chunk of 64 logits is scanned
+// for the next such lane after the one just taken, with the last slot read
+// again after every insertion, so a logit is skipped exactly when the loop
+// would skip it. The insertion point is one past the highest slot below k-1
+// that is not less than v (the while loop's stop), 0 if there is none; the
+// slots from there to k-2 move down by one and slot k-1 falls off.
+__device__ void topk_in_order(const float *__restrict__ y, int n, int k, float *__restrict__ vals,
+                              int32_t *__restrict__ idx, int lane) {
+    uint32_t sv = __float_as_uint(-1e30f);
+    int si = 0;
+    constexpr int U = 8;                      // chunks of 64 loaded at once
+    for (int c0 = 0; c0 < n; c0 += 64 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = c0 + 64 * u + lane;
+            v[u] = y[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int base = c0 + 64 * u;
+            if (base >= n) break;
+            const bool in = base + lane < n;
+            int last = -1;
+            for (;;) {
+                const float thr = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)sv, k - 1));
+                const unsigned long long m = __ballot(in && lane > last && !(v[u] <= thr));
+                if (!m) break;
+                const int b = __builtin_ctzll(m);
+                const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[u]), b));
+                const unsigned long long stop = __ballot(lane < k - 1 && !(__uint_as_float(sv) < x));
+                const int pos = stop ? 64 - __builtin_clzll(stop) : 0;
+                const uint32_t above = (uint32_t)__shfl((int)sv, lane - 1);
+                const int above_i = __shfl(si, lane - 1);
+                if (lane == pos) {
+                    sv = __float_as_uint(x);
+                    si = base + b;
+                } else if (lane > pos && lane < k) {
+                    sv = above;
+                    si = above_i;
+                }
+                last = b;
+            }
+        }
+    }
+    if (lane < k) {
+        vals[lane] = __uint_as_float(sv);
+        idx[lane] = si;
+    }
+}
+
+__global__ __launch_bounds__(1024) void topk_stage2(const float *__restrict__ y, int n,
+                                                    const unsigned long long *lists, int nlists, int k,
+                                                    float *__restrict__ vals,
                                                     int32_t *__restrict__ idx) {
     extern __shared__ __attribute__((aligned(16))) unsigned long long lk[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (__syncthreads_or(t < nlists && lists[(size_t)t * TOPK_LIST] == NAN_MARK)) {
+        if (wave == 0) topk_in_order(y, n, k, vals, idx, lane);
+        return;
+    }
     int np = 1;
     while (np < nlists) np <<= 1;
     {
@@ -186,7 +259,7 @@ hipError_t launch_topk(const float *y, int n, int k, float *vals, int32_t *idx, 
     int np = 1;
     while (np < nlists) np <<= 1;
     const size_t lds = (size_t)np * TOPK_LIST * sizeof(unsigned long long);
-    hipLaunchKernelGGL(topk_stage2, dim3(1), dim3(1024), lds, stream, y, lists, nlists, k, vals, idx);
+    hipLaunchKernelGGL(topk_stage2, dim3(1), dim3(1024), lds, stream, y, n, lists, nlists, k, vals, idx);
     return hipGetLastError();
 }
 

@@ -104,13 +104,22 @@ def decode_chain() -> list[Matrix]:
 
 
 CHAIN_STEPS = 400
-GEMM_M = (1, 4, 8, 16, 24, 64)
+GEMM_M = (1, 2, 4, 8, 16, 24, 64)
 GEMM_SHAPES = (LAYER_SHAPES[2], LAYER_SHAPES[3])   # gate+up 16384x2048, down 2048x8192
 
 
 def gemm_activation(m_rows: int, k: int) -> np.ndarray:
     """M rows of fp32 N(0, 1), seed 40 + M."""
     return normal_f32((m_rows, k), 40 + m_rows)
+
+
+# A prompt through the decode chain's matrices at once (the M > 1 path).
+PREFILL_M = 24
+
+
+def prefill_activation(index: int, m_rows: int, k: int) -> np.ndarray:
+    """m_rows prompt rows for matrix `index` of decode_chain(): fp32 N(0, 1), seed 3000 + index."""
+    return normal_f32((m_rows, k), 3000 + index)
 
 
 def chain_weight_bytes() -> int:

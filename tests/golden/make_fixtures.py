@@ -18,8 +18,11 @@ weights, then float32. Seeds:
   config 2  LM head 128256x2048: weights 30, activation 31
   config 3  16 layers x (q|k|v, o, gate|up, down) + LM head: weights
             1000 + 4 l + j (LM head 1064), activations 2000 + 4 l + j (2064)
-  config 4  gate|up and down of config 1 at M = 1, 4, 8, 16, 24, 64
+  config 4  gate|up and down of config 1 at M = 1, 2, 4, 8, 16, 24, 64
             activation rows: default_rng(40 + M).standard_normal((M, K))
+  config3_prefill24
+            config 3's weights, a 24-token prompt per matrix: activation rows
+            default_rng(3000 + j).standard_normal((24, K)) for matrix j
 """
 
 from __future__ import annotations
@@ -59,9 +62,10 @@ def quantized_weights(m: cf.Matrix) -> np.ndarray:
     return blocks
 
 
-def matrix_record(m: cf.Matrix, cross_check: bool) -> dict:
+def matrix_record(m: cf.Matrix, cross_check: bool, blocks: np.ndarray | None = None) -> dict:
     x = cf.activation(m)
-    blocks = quantized_weights(m)
+    if blocks is None:
+        blocks = quantized_weights(m)
     xq, xd = C.quantize_q8_0(x)
     y = C.gemv_q4_0(blocks, m.k, xq, xd)
     if cross_check:
@@ -85,6 +89,14 @@ def gemm_record(m: cf.Matrix, mrows: int, blocks: np.ndarray, cross_check: bool)
             "xq": sha(xq), "y": sha(y), "y_head": head_hex(y)}
 
 
+def prefill_record(index: int, m: cf.Matrix, blocks: np.ndarray, mrows: int) -> dict:
+    x = cf.prefill_activation(index, mrows, m.k)
+    xq, xd = C.quantize_q8_0_rows(x)
+    y = C.gemm_q4_0_rows(blocks, m.k, xq, xd)
+    return {"name": m.name, "m": mrows, "rows": m.rows, "k": m.k, "x_seed": 3000 + index,
+            "xq": sha(xq), "y": sha(y), "y_head": head_hex(y)}
+
+
 def build() -> dict:
     t0 = time.time()
     out = {"contract": O.CONTRACT_VERSION,
@@ -94,7 +106,13 @@ def build() -> dict:
     print(f"configs 0-1 done ({time.time() - t0:.1f} s)", flush=True)
     out["config2"] = [matrix_record(cf.LM_HEAD, False)]
     print(f"config 2 done ({time.time() - t0:.1f} s)", flush=True)
-    out["config3"] = [matrix_record(m, False) for m in cf.decode_chain()]
+    c3, p24 = [], []
+    for j, m in enumerate(cf.decode_chain()):
+        blocks = quantized_weights(m)
+        c3.append(matrix_record(m, False, blocks))
+        p24.append(prefill_record(j, m, blocks, cf.PREFILL_M))
+    out["config3"] = c3
+    out["config3_prefill24"] = p24
     print(f"config 3 done ({time.time() - t0:.1f} s)", flush=True)
     g4 = []
     for m in cf.GEMM_SHAPES:

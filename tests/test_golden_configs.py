@@ -42,3 +42,13 @@ def test_fixtures_reproduce_from_the_oracle():
     with open(FIXTURES) as f:
         committed = json.load(f)
     assert make_fixtures.build() == committed
+
+
+def test_gen_vectors_reproduce_from_the_oracle():
+    """The reference's exactness cases (gen_vectors.py, one default_rng(4) stream)
+    recomputed by both oracle implementations match the committed digests."""
+    import make_gen_vectors
+    with open(os.path.join(HERE, "golden", "gen_vectors.json")) as f:
+        committed = json.load(f)
+    assert make_gen_vectors.build() == committed
+    assert [c["name"] for c in committed["cases"]][:5] == ["k256_n16", "k2048_n64", "k8192_n16", "k256_n32", "k8192_n32"]

@@ -8,7 +8,10 @@ pool first (board/kv260gemv/bench_gemv2.c:63)."""
 from __future__ import annotations
 
 import ctypes
+import hashlib
+import json
 import os
+import sys
 
 import numpy as np
 import pytest
@@ -16,6 +19,11 @@ import pytest
 import c_oracle as C
 import q4_0_oracle as O
 from gpu_helpers import assert_bytes_equal
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+
+import make_gen_vectors as GV  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -159,3 +167,90 @@ def test_v2_fetch_then_mac(board, rows, k):
     assert_bytes_equal(_read_y(L, y_host, rows), want, "gemv2 fetch + mac")
     L.gemv2_dev_close(ctypes.byref(d2))
     pool.used = 0
+
+
+def _v2_check_case(L, pool, blocks, x_eng, rows, k):
+    """bench_gemv2.c:47-79 (check_case): x and a 0xAA-poisoned y in the pool,
+    the matrix in four 64 KB-aligned port regions with ports 1 and 3 offset by
+    16 KB (new_mat, :29-40), rows placed by the chunk formula (put_row, :41-43),
+    one fetch + MAC, the outputs read back after invalidate."""
+    x_host, xp = _alloc(L, pool, np.concatenate([x_eng, np.zeros(64, np.uint8)]))
+    y_host, yp = _poisoned_y(L, pool, rows)
+    quarter = rows // 4 * k // 32 * 18
+    ports, phys = [], []
+    for p in range(4):
+        off = (p & 1) * (16 << 10)
+        host = L.udmabuf_alloc(ctypes.byref(pool), quarter + off, 64 << 10)
+        assert host, "pool full"
+        ports.append(np.ctypeslib.as_array((ctypes.c_uint8 * quarter).from_address(host + off)))
+        phys.append(pool.phys + (host - pool.base) + off)
+    raw = blocks.reshape(rows, k // 256, 144)
+    for r in range(rows):
+        for c in range(k // 256):
+            o, port = _chunk_offset(r, c, rows, k)
+            ports[port][o:o + 144] = raw[r, c]
+    for p in range(4):
+        L.udmabuf_clean(ports[p].ctypes.data, quarter)
+    d2 = Dev2()
+    assert L.gemv2_dev_open(ctypes.byref(d2)) == 0
+    assert L.gemv2_mac_idle(ctypes.byref(d2)) == 1
+    L.gemv2_fetch_start(ctypes.byref(d2), (u64 * 4)(*phys), k, rows)
+    L.gemv2_mac_start(ctypes.byref(d2), xp, yp, k, rows)
+    L.gemv2_mac_wait(ctypes.byref(d2))
+    y = _read_y(L, y_host, rows)
+    L.gemv2_dev_close(ctypes.byref(d2))
+    return y
+
+
+@pytest.fixture(scope="module")
+def gen_vectors():
+    """The reference's exactness cases (gen_vectors.py), regenerated by the
+    oracle and checked against the committed digests before any GPU call."""
+    with open(os.path.join(HERE, "golden", "gen_vectors.json")) as f:
+        pinned = json.load(f)
+    out = {}
+    for group, cases in (("cases", GV.CASES), ("shard_cases", GV.SHARD_CASES)):
+        for want, (k, rows, blocks, x_eng, y, _, _) in zip(pinned[group], GV.draw(cases)):
+            sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+            assert (want["k"], want["rows"]) == (k, rows)
+            assert (sha(blocks), sha(x_eng), sha(y)) == (want["w"], want["x"], want["y"]), want["name"]
+            out[want["name"]] = (k, rows, blocks, x_eng, y)
+    return out
+
+
+GEN_VECTOR_NAMES = ([f"k{k}_n{rows}" for k, rows in GV.CASES] +
+                    [f"k{k}_n{rows}" for k, rows in GV.SHARD_CASES])
+
+
+def _v1_run(L, pool, blocks, x_eng, rows, k):
+    """The v1 engine's exactness run (evidence 0006-bench-gemv-kv260-01.txt:2-5):
+    the rows contiguous at a 64 KB-aligned address, x, a poisoned y, one
+    gemv_dev_run."""
+    _, wp = _alloc(L, pool, blocks.reshape(-1), 64 << 10)
+    _, xp = _alloc(L, pool, x_eng)
+    y_host, yp = _poisoned_y(L, pool, rows)
+    d = Dev()
+    assert L.gemv_dev_open(ctypes.byref(d)) == 0
+    L.gemv_dev_run(ctypes.byref(d), wp, xp, yp, k, rows)
+    y = _read_y(L, y_host, rows)
+    L.gemv_dev_close(ctypes.byref(d))
+    return y
+
+
+@pytest.mark.parametrize("name", GEN_VECTOR_NAMES)
+def test_gen_vectors_exactness(board, gen_vectors, name):
+    """Every case of gen_vectors.py, plus the shard shapes the board run names
+    (0013-bench-gemv2.txt:1): through the v1 engine's gemv_dev_run (rows % 16,
+    as the v1 bench ran the first three), and through gemv2_fetch_start /
+    gemv2_mac_start as check_case issues them wherever gemv2's rows % 32
+    holds (gemv2_dev.h:14). Bit-exact, every row written."""
+    L, pool = board
+    k, rows, blocks, x_eng, want = gen_vectors[name]
+    assert rows % 16 == 0 and k % 256 == 0
+    got = _v1_run(L, pool, blocks, x_eng, rows, k)
+    pool.used = 0
+    assert_bytes_equal(got, want, f"gen_vectors {name}, v1")
+    if rows % 32 == 0:
+        got = _v2_check_case(L, pool, blocks, x_eng, rows, k)
+        pool.used = 0
+        assert_bytes_equal(got, want, f"gen_vectors {name}, gemv2")

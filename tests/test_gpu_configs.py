@@ -108,18 +108,26 @@ def test_config2_lm_head_three_copies(gpu):
         assert int(np.argmax(got)) == rec["argmax"]
 
 
-def test_config3_decode_chain_400_steps(gpu):
+@pytest.fixture(scope="module")
+def chain_blocks(gpu):
+    """Config 3's 65 weight matrices, quantized on the GPU once for every
+    config-3 test and checked against their digests."""
+    mats = []
+    for m, rec in zip(cf.decode_chain(), FIX["config3"]):
+        b = device_blocks(gpu, m)
+        assert sha(host(b)) == rec["q4_0"], f"{m.name}: Q4_0 weights"
+        mats.append(b)
+    return mats
+
+
+def test_config3_decode_chain_400_steps(gpu, chain_blocks):
     """The 65-matrix chain: byte-exact after step 0 and after step 399, through the
     dependent chain entry point, and once through the batch."""
     import torch
     chain, recs = cf.decode_chain(), FIX["config3"]
-    mats, xs, ys = [], [], []
-    for m, rec in zip(chain, recs):
-        b = device_blocks(gpu, m)
-        assert sha(host(b)) == rec["q4_0"], f"{m.name}: Q4_0 weights"
-        mats.append(b)
-        xs.append(dev(cf.activation(m)))
-        ys.append(poisoned_f32(m.rows))
+    mats = chain_blocks
+    xs = [dev(cf.activation(m)) for m in chain]
+    ys = [poisoned_f32(m.rows) for m in chain]
     shapes = [(m.rows, m.k) for m in chain]
     steps = step_array(mats, xs, ys, shapes)
     ptr = ctypes.cast(steps, ctypes.c_void_p)
@@ -144,16 +152,14 @@ def test_config3_decode_chain_400_steps(gpu):
     check("batch")
 
 
-def test_config3_one_launch_chain(gpu):
+def test_config3_one_launch_chain(gpu, chain_blocks):
     """The 65-matrix chain as one cooperative launch (W4A8_CHAIN_ONE_LAUNCH):
     byte-exact after the first launch and after 50 more, no wait given up."""
     import torch
     chain, recs = cf.decode_chain(), FIX["config3"]
-    mats, xs, ys = [], [], []
-    for m in chain:
-        mats.append(device_blocks(gpu, m))
-        xs.append(dev(cf.activation(m)))
-        ys.append(poisoned_f32(m.rows))
+    mats = chain_blocks
+    xs = [dev(cf.activation(m)) for m in chain]
+    ys = [poisoned_f32(m.rows) for m in chain]
     steps = step_array(mats, xs, ys, [(m.rows, m.k) for m in chain])
     ptr = ctypes.cast(steps, ctypes.c_void_p)
     L = gpu.lib()
@@ -171,6 +177,19 @@ def test_config3_one_launch_chain(gpu):
         assert L.w4a8_chain_timeouts() == 0
     finally:
         L.w4a8_chain_set_mode(1)
+
+
+def test_config3_prefill24(gpu, chain_blocks):
+    """A 24-token prompt through the chain's 65 matrices (quantize the rows, then
+    the M > 1 GEMM), every output byte-exact against the oracle's digests."""
+    chain, recs = cf.decode_chain(), FIX["config3_prefill24"]
+    for j, (m, b, rec) in enumerate(zip(chain, chain_blocks, recs)):
+        x_rows = gpu.quantize_q8_0_engine(dev(cf.prefill_activation(j, cf.PREFILL_M, m.k)))
+        assert sha(host(x_rows)[:, :m.k]) == rec["xq"], m.name
+        y = poisoned_f32((cf.PREFILL_M, m.rows))
+        gpu.gemm_engine(b, m.k, x_rows, out=y)
+        got = host(y)
+        assert sha(got) == rec["y"], f"prefill {m.name}: head {got.reshape(-1)[:4].view(np.uint32)}"
 
 
 def test_config4_m_sweep(gpu):

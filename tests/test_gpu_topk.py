@@ -87,3 +87,49 @@ def test_rejections(gpu):
     assert L.w4a8_topk(None, 1000, 8, v.data_ptr(), i.data_ptr(), ws.data_ptr(), nbytes, None) == -1
     assert call(1000, 8) == 0
     torch.cuda.synchronize()
+
+
+def _check_nan(gpu, y, k, label):
+    """Indices equal, NaN slots in the same places, every other value bit for bit."""
+    vals, idx = gpu.topk(dev(y), k)
+    want_v, want_i = C.topk(y, k)
+    got_v, got_i = host(vals), host(idx)
+    assert np.array_equal(got_i, want_i), (label, got_i[:8], want_i[:8])
+    assert np.array_equal(np.isnan(got_v), np.isnan(want_v)), label
+    ok = ~np.isnan(want_v)
+    assert np.array_equal(got_v[ok].view(np.uint32), want_v[ok].view(np.uint32)), label
+    # A NaN slot holds y's own NaN, bit for bit.
+    for j in np.flatnonzero(~ok):
+        assert got_v[j:j + 1].view(np.uint32)[0] == y[got_i[j]:got_i[j] + 1].view(np.uint32)[0], label
+
+
+@pytest.mark.parametrize("n,k,seed,where", [(128256, 40, 20, "spread"), (128256, 64, 21, "last"),
+                                            (128256, 1, 22, "spread"), (5000, 17, 23, "runs"),
+                                            (1025, 64, 24, "first"), (64, 64, 25, "spread"),
+                                            (262144, 40, 26, "late")])
+def test_nan_logits_follow_the_reference_loop(gpu, n, k, seed, where):
+    """NaN logits take the last slot and let the next logit in, as the
+    reference's loop does (tp_llama.cpp:902-908), wherever they stand."""
+    print(f"topk NaN n={n} k={k} seed={seed} where={where}", flush=True)
+    rng = np.random.default_rng(seed)
+    y = _logits(n, seed, grid=2 if where == "runs" else 0)
+    if where == "spread":
+        y[rng.integers(0, n, 12)] = np.nan
+        y[rng.integers(0, n, 6)] = -np.inf
+    elif where == "last":
+        y[-1] = np.nan
+    elif where == "first":
+        y[0] = np.nan
+        y[1] = -np.inf
+    elif where == "runs":
+        y[100:104] = np.nan
+        y[2000:2002] = [np.nan, -np.inf]
+        y[4999] = np.nan
+    else:
+        y[n - 5000] = np.nan
+        y[n - 4999] = F32(-3e30)
+    y[rng.integers(0, n, 2)] = F32(np.frombuffer(np.uint32(0xFFC00123).tobytes(), np.float32)[0])  # a payload
+    _check_nan(gpu, y, k, f"n={n} k={k} {where}")
+    clean = y.copy()
+    clean[np.isnan(clean)] = 0.0
+    _check(gpu, clean, k, f"n={n} k={k} without NaN")          # the parallel path again afterwards

@@ -60,6 +60,31 @@ def test_loop_matches_definition(n, k, seed, grid):
     assert same(C.topk(y, k), by_definition(y, k))
 
 
+NAN = np.nan
+
+
+@pytest.mark.parametrize("y,k,vals,idx", [
+    # A NaN is admitted (v <= NaN is false) into the last slot, evicting the
+    # k-th candidate held then; the next logit enters whatever its value.
+    ([3, 2, NAN, 1], 2, [3, 1], [0, 3]),                    # 2 is lost to the NaN, 1 takes its place
+    ([1, NAN, 0.5], 2, [1, 0.5], [0, 2]),
+    ([5, 4, NAN], 2, [5, NAN], [0, 2]),                     # a NaN at the end stays in the last slot
+    ([NAN, -np.inf], 2, [-1e30, -np.inf], [0, 1]),          # -inf enters after a NaN, below the sentinel
+    ([NAN, -np.inf, 2], 2, [2, -1e30], [2, 0]),             # ... and is the one the next value evicts
+    ([4, NAN, NAN, 3], 3, [4, 3, -1e30], [0, 3, 0]),        # each NaN replaces the last slot again
+    ([NAN, 9, 8], 1, [9], [1]),                             # k = 1: the NaN is the only slot, then 9
+    ([2, 7, NAN, 6, 5], 3, [7, 6, 5], [1, 3, 4]),
+])
+def test_hand_worked_nan(y, k, vals, idx):
+    """Worked by hand through tp_llama.cpp:902-908 with IEEE comparisons."""
+    got = C.topk(np.array(y, dtype=np.float32), k)
+    want = (np.array(vals, dtype=np.float32), np.array(idx, dtype=np.int32))
+    assert np.array_equal(got[1], want[1]), (got, want)
+    assert np.array_equal(np.isnan(got[0]), np.isnan(want[0]))
+    ok = ~np.isnan(want[0])
+    assert np.array_equal(got[0][ok].view(np.uint32), want[0][ok].view(np.uint32)), (got, want)
+
+
 def test_first_candidate_is_the_argmax_scan():
     rng = np.random.default_rng(9)
     y = (np.round(rng.standard_normal(20000) * 2) / 2).astype(np.float32)
