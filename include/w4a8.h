@@ -100,6 +100,18 @@ size_t w4a8_topk_workspace_bytes(int n);
 int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *workspace, size_t workspace_bytes,
               void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): w4a8_topk with its workspace in the library's own device
+ * array, one per device (128 KiB, held until the process ends), so the call
+ * allocates nothing. Same candidates, bit for bit, as w4a8_topk.
+ * 1 <= n <= W4A8_TOPK_NO_ALLOC_MAX_N (larger n: W4A8_ERR_SHAPE), 1 <= k <= 64.
+ * The array belongs to the device current at the call; every call on that
+ * device shares it, so calls that overlap on one device (two streams, two
+ * threads) race and may return wrong candidates: serialize them. */
+#define W4A8_TOPK_NO_ALLOC_MAX_N 262144
+int w4a8_topk_no_alloc(const float *y, int n, int k, float *vals, int32_t *idx, void *stream);
+
 /* The reference's producers of the GEMV input, fused into the GEMV's own
  * activation staging (board/tp/tp_llama.cpp, computed as it does):
  *   rmsnorm (:557-569): h = x * (1 / sqrtf((float)(ss / k) + eps)) * norm_w,

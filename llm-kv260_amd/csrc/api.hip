@@ -115,6 +115,13 @@ int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *wor
     return hip_status(launch_topk(y, n, k, vals, idx, workspace, (hipStream_t)stream));
 }
 
+int w4a8_topk_no_alloc(const float *y, int n, int k, float *vals, int32_t *idx, void *stream) {
+    if (!y || !vals || !idx) return W4A8_ERR_NULL;
+    if (n < 1 || n > W4A8_TOPK_NO_ALLOC_MAX_N || k < 1 || k > 64) return W4A8_ERR_SHAPE;
+    if (!aligned(y, 4) || !aligned(vals, 4) || !aligned(idx, 4)) return W4A8_ERR_ALIGN;
+    return hip_status(launch_topk_no_alloc(y, n, k, vals, idx, (hipStream_t)stream));
+}
+
 // The fused rmsnorm stages x's float64 squares in LDS: k <= 8192.
 constexpr int RMS_FUSED_MAX_K = 8192;
 

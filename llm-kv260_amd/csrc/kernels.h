@@ -64,6 +64,9 @@ hipError_t launch_topk(const float *y, int n, int k, float *vals, int32_t *idx, 
                        hipStream_t stream);
 size_t topk_workspace_bytes(int n);
 int topk_max_n();
+// Same, the lists in the library's own device array (one per device, no
+// allocation): calls that overlap on one device race on it.
+hipError_t launch_topk_no_alloc(const float *y, int n, int k, float *vals, int32_t *idx, hipStream_t stream);
 
 // y[m][rows] for m activation rows in engine layout (row stride K + K/8 bytes).
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, float *y, hipStream_t stream);

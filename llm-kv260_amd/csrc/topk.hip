@@ -32,6 +32,9 @@
 // pass over y by a single wave.
 #include "kernels.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace w4a8 {
 
 namespace {
@@ -237,6 +240,39 @@ __global__ __launch_bounds__(1024) void topk_stage2(const float *__restrict__ y,
     }
 }
 
+// The stage-1 lists of the largest input (TOPK_MAX_LISTS lists of 64 keys,
+// 128 KiB) for launch_topk_no_alloc: one copy per device, held until the
+// process ends. Host code never passes the name itself to a kernel (on the
+// host it is a stand-in, not a device address): it passes the address
+// hipGetSymbolAddress gives for the current device.
+static __device__ __align__(256) unsigned long long scratch[TOPK_MAX_LISTS * TOPK_LIST];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::atomic<void *> g_scratch[SCRATCH_MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the first call on it) and kept.
+hipError_t scratch_of_current_device(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return hipErrorInvalidDevice;
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return e;
+            if (!p) return hipErrorInvalidSymbol;
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
+
 }  // namespace
 
 size_t topk_workspace_bytes(int n) {
@@ -261,6 +297,17 @@ hipError_t launch_topk(const float *y, int n, int k, float *vals, int32_t *idx, 
     const size_t lds = (size_t)np * TOPK_LIST * sizeof(unsigned long long);
     hipLaunchKernelGGL(topk_stage2, dim3(1), dim3(1024), lds, stream, y, n, lists, nlists, k, vals, idx);
     return hipGetLastError();
+}
+
+static_assert(sizeof(unsigned long long) * TOPK_MAX_LISTS * TOPK_LIST == 131072,
+              "scratch holds the lists of the largest input launch_topk takes");
+
+hipError_t launch_topk_no_alloc(const float *y, int n, int k, float *vals, int32_t *idx, hipStream_t stream) {
+    if (n < 1 || n > topk_max_n() || k < 1 || k > TOPK_LIST) return hipErrorInvalidValue;
+    void *lists = nullptr;
+    const hipError_t e = scratch_of_current_device(&lists);
+    if (e != hipSuccess) return e;
+    return launch_topk(y, n, k, vals, idx, lists, stream);
 }
 
 }  // namespace w4a8

@@ -41,7 +41,7 @@ EXPORTS = (
     "w4a8_quantize_q8_0", "w4a8_quantize_q8_0_blocks", "w4a8_quantize_q4_0", "w4a8_gemm",
     "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
     "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
-    "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk", "w4a8_gemv_gate_up_silu",
+    "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk", "w4a8_topk_no_alloc", "w4a8_gemv_gate_up_silu",
     "w4a8_chain_set_mode", "w4a8_chain_set_spin_limit", "w4a8_chain_timeouts",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
@@ -121,6 +121,8 @@ def lib() -> ctypes.CDLL:
     L.w4a8_topk_workspace_bytes.restype = ctypes.c_size_t
     L.w4a8_topk.argtypes = [p, i, i, p, p, p, ctypes.c_size_t, p]
     L.w4a8_topk.restype = i
+    L.w4a8_topk_no_alloc.argtypes = [p, i, i, p, p, p]
+    L.w4a8_topk_no_alloc.restype = i
     L.w4a8_gemv_gate_up_silu.argtypes = [p, p, p, f32, p, i, i, p]
     L.w4a8_gemv_gate_up_silu.restype = i
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):

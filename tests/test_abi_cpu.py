@@ -51,6 +51,19 @@ def test_every_declared_symbol_is_exported():
     assert declared <= exported
 
 
+def test_topk_no_alloc_checks_come_before_the_device():
+    """The no-allocation top-k refuses sizes beyond its array, and bad pointers,
+    without any HIP call (no GPU here)."""
+    L = kv260gemv.lib()
+    fake = 0x10000
+    assert L.w4a8_topk_no_alloc(fake, 262145, 40, fake, fake, None) == -2
+    assert L.w4a8_topk_no_alloc(fake, 0, 40, fake, fake, None) == -2
+    assert L.w4a8_topk_no_alloc(fake, 1000, 0, fake, fake, None) == -2
+    assert L.w4a8_topk_no_alloc(fake, 1000, 65, fake, fake, None) == -2
+    assert L.w4a8_topk_no_alloc(None, 1000, 40, fake, fake, None) == -1
+    assert L.w4a8_topk_no_alloc(fake + 2, 1000, 40, fake, fake, None) == -3
+
+
 def test_size_helpers():
     L = kv260gemv.lib()
     assert L.w4a8_q4_0_row_bytes(2048) == 1152
