@@ -130,6 +130,9 @@ int w4a8_gemv_rmsnorm(const void *w, const float *x, const float *norm_w, float 
                       void *stream);
 int w4a8_gemv_rmsnorm_argmax(const void *w, const float *x, const float *norm_w, float eps, float *y, int rows, int k,
                              int32_t *argmax, void *workspace, size_t workspace_bytes, void *stream);
+/* silu(gate) * up in down's own staging: the same bytes as w4a8_silu_mul_q8_0
+ * then w4a8_gemv, but slower than that pair and than w4a8_gemv_gate_up_silu
+ * (each workgroup recomputes all k exponentials); prefer those. */
 int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, int k, void *stream);
 
 /* The gate|up GEMV with silu as its epilogue: y = W Q8_0(h) over rows = 2n

@@ -9,6 +9,8 @@
 //   graph     the device-side time per call: N w4a8_gemv launches captured in
 //             one HIP graph, replayed, HIP events around the replay, / N
 //             (the kernel plus the launch boundary, no host in the loop)
+//   start, wait  raw's two halves: gemv_dev_start (the enqueue) and gemv_dev_wait
+//   launch_poll  w4a8_gemv on a stream, waited for by polling hipStreamQuery
 //   q8        the standalone Q8_0 quantize of a float32 x (w4a8_quantize_q8_0,
 //             the reference's q8ref / q8neon columns run on the CPU): host-
 //             visible launch + stream sync, best and mean, and device-side
@@ -149,6 +151,26 @@ int main(int argc, char **argv) {
             udmabuf_invalidate(y, ybytes);
             inval.add(now() - a);
         }
+        // The parts of raw: the enqueue alone (gemv_dev_start), then the wait;
+        // and the same launch waited for by polling the stream instead.
+        Stat enq, wait, poll;
+        for (int r = 0; r < reps; ++r) {
+            double a = now();
+            gemv_dev_start(&dev, wp, xp, yp, sh.k, sh.rows);
+            const double b = now();
+            gemv_dev_wait(&dev);
+            enq.add(b - a);
+            wait.add(now() - b);
+        }
+        for (int r = 0; r < reps; ++r) {
+            const double a = now();
+            if (w4a8_gemv((const void *)wp, (const void *)xp, (float *)yp, sh.rows, sh.k, s)) DIE("w4a8_gemv");
+            hipError_t q;
+            while ((q = hipStreamQuery(s)) == hipErrorNotReady) {
+            }
+            HIP_OK(q);
+            poll.add(now() - a);
+        }
         // q8: the standalone quantize, launch + sync, host-visible.
         for (int r = 0; r < 5; ++r)
             if (w4a8_quantize_q8_0((const float *)xfp, (void *)xqp, sh.k, 1, s)) DIE("quantize %s", sh.name);
@@ -192,10 +214,11 @@ int main(int argc, char **argv) {
         snprintf(buf, sizeof buf,
                  "%s{\"shape\": \"%s\", \"k\": %d, \"rows\": %d, \"weight_mb\": %.3f, \"raw_best_us\": %.2f, "
                  "\"raw_mean_us\": %.2f, \"raw_gbps\": %.2f, \"graph_us\": %.3f, \"clean_x_us\": %.2f, "
-                 "\"inval_y_us\": %.2f, \"q8_host_best_us\": %.2f, \"q8_host_mean_us\": %.2f, \"q8_graph_us\": %.3f}",
+                 "\"inval_y_us\": %.2f, \"q8_host_best_us\": %.2f, \"q8_host_mean_us\": %.2f, \"q8_graph_us\": %.3f, "
+                 "\"start_us\": %.2f, \"wait_us\": %.2f, \"launch_poll_us\": %.2f}",
                  si ? ", " : "", sh.name, sh.k, sh.rows, wbytes / 1e6, raw.best_us(), raw.mean_us(),
                  wbytes / raw.best / 1e9, gemv_graph, clean.best_us(), inval.best_us(), q8host.best_us(),
-                 q8host.mean_us(), q8_graph);
+                 q8host.mean_us(), q8_graph, enq.best_us(), wait.best_us(), poll.best_us());
         out += buf;
         fprintf(stderr, "call_costs: %-8s raw %.2f us (mean %.2f), graph %.3f us, q8 %.2f us host / %.3f us graph\n",
                 sh.name, raw.best_us(), raw.mean_us(), gemv_graph, q8host.best_us(), q8_graph);
