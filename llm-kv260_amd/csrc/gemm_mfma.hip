@@ -96,8 +96,10 @@ struct GemmParams {
 
 // Geometry of one instance: MT token tiles per item, D chunks per round, P
 // rounds in flight, OCC workgroups per CU (the LDS of one is then at most
-// LDS_MAX / OCC; with two, each SIMD runs four waves).
-template <int MT, int D, int P, int OCC>
+// LDS_MAX / OCC; with two, each SIMD runs four waves), NRL live rows per item
+// (16, or 8 where 16-row items would leave CUs idle: the MFMA's row columns
+// 8..15 then compute on whatever their LDS rows hold and are never stored).
+template <int MT, int D, int P, int OCC, int NRL>
 struct Geo {
     static constexpr int TT = 16 * MT;                      // tokens per item
     static constexpr int WP = D * CHUNK_BYTES + 16;         // LDS bytes per weight row (padded: bank spread)
@@ -123,7 +125,8 @@ struct Geo {
     static_assert(LDS <= BUDGET, "round buffers exceed the LDS budget");
     static_assert(BUF < 65536, "a round buffer offset must fit an LDS instruction's immediate");
     // 16-byte pieces of a round and the load slots per thread that carry them.
-    static constexpr int W_PIECES = NR * D * 9;
+    static_assert(NRL == 16 || NRL == 8, "an item is 16 or 8 rows");
+    static constexpr int W_PIECES = NRL * D * 9;
     static constexpr int X_PIECES = TT * D * 16;
     static constexpr int XD_PIECES = TT * D * 2;
     static constexpr int SW = (W_PIECES + GTHREADS - 1) / GTHREADS;
@@ -140,9 +143,9 @@ struct Regs {
     u32x4 d[SD];
 };
 
-template <int MT, int D, int P, int OCC, bool ODD>
+template <int MT, int D, int P, int OCC, int NRL, bool ODD>
 struct Kernel {
-    using G = Geo<MT, D, P, OCC>;
+    using G = Geo<MT, D, P, OCC, NRL>;
     using R = Regs<G::SW, G::SX, G::SD>;
 
     // Per-thread offsets of its load slots and outputs, fixed for the whole
@@ -195,7 +198,7 @@ struct Kernel {
         for (int o = 0; o < G::OUTS; ++o) {
             const int idx = o * GTHREADS + tid;
             const int tok = idx / NR, row = idx - tok * NR;
-            const bool has = idx < G::TT * NR;
+            const bool has = idx < G::TT * NR && row < NRL;
             s.o_ex[o] = tok * G::EXP + row;
             s.o_tok[o] = has ? tok : 0x7fffffff;
             s.o_row[o] = row;
@@ -329,7 +332,7 @@ struct Kernel {
         const int RPI = C / D;                                  // rounds per item (D divides C)
         const int row_bytes = C * CHUNK_BYTES;
         // Items are (row group, token group) pairs, row groups fastest.
-        const int row_groups = (Pm.rows + NR - 1) / NR;
+        const int row_groups = (Pm.rows + NRL - 1) / NRL;
         const int items = row_groups * ((Pm.m + G::TT - 1) / G::TT);
         const int GD = gridDim.x;
         const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / GD + 1 : 0;
@@ -357,7 +360,7 @@ struct Kernel {
             }
         };
         auto load_at = [&](const Pos &p, R &rg) {
-            load(Pm, s, row_bytes, p.rg_i * NR, p.tg_i * G::TT, p.ss * D, p.kk < my_items, rg);
+            load(Pm, s, row_bytes, p.rg_i * NRL, p.tg_i * G::TT, p.ss * D, p.kk < my_items, rg);
         };
         const Pos first{0, 0, (int)blockIdx.x % row_groups, (int)blockIdx.x / row_groups};
         const uint32_t y_total = (uint32_t)((size_t)Pm.m * Pm.rows * 4);
@@ -387,7 +390,7 @@ struct Kernel {
                 const int q = q0 + d;
                 const bool live = cp.kk < my_items;
                 const bool item_end = live && cp.ss == RPI - 1;
-                const int n0 = cp.rg_i * NR, m0 = cp.tg_i * G::TT;
+                const int n0 = cp.rg_i * NRL, m0 = cp.tg_i * G::TT;
                 float *ex = reinterpret_cast<float *>(lds + G::EX_OFF + (G::EXN == 2 ? (cp.kk & 1) * G::EX_BYTES : 0));
                 if (live) compute(lds + (q & 1) * G::BUF, acc);
                 if (item_end) {
@@ -433,14 +436,14 @@ struct Kernel {
     }
 };
 
-template <int MT, int D, int P, int OCC>
+template <int MT, int D, int P, int OCC, int NRL>
 __global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(2 * OCC, 2 * OCC)))
 void gemm_mfma_kernel(GemmParams Pm) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if ((threadIdx.x >> 6) & 1)
-        Kernel<MT, D, P, OCC, true>::run(Pm, lds);
+        Kernel<MT, D, P, OCC, NRL, true>::run(Pm, lds);
     else
-        Kernel<MT, D, P, OCC, false>::run(Pm, lds);
+        Kernel<MT, D, P, OCC, NRL, false>::run(Pm, lds);
 }
 
 #ifndef W4A8_GEMM_DEPTH
@@ -448,38 +451,39 @@ void gemm_mfma_kernel(GemmParams Pm) {
 #endif
 constexpr int DEPTH = W4A8_GEMM_DEPTH;
 
-template <int MT, int D, int OCC>
+template <int MT, int D, int OCC, int NRL = 16>
 hipError_t launch_geo(const GemmParams &Pm, hipStream_t stream) {
-    using G = Geo<MT, D, DEPTH, OCC>;
-    const void *fn = reinterpret_cast<const void *>(&gemm_mfma_kernel<MT, D, DEPTH, OCC>);
+    using G = Geo<MT, D, DEPTH, OCC, NRL>;
+    const void *fn = reinterpret_cast<const void *>(&gemm_mfma_kernel<MT, D, DEPTH, OCC, NRL>);
     hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
     if (e != hipSuccess) return e;
     int per_cu = 0;
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, GTHREADS, G::LDS);
     if (e != hipSuccess) return e;
     if (per_cu < 1) per_cu = 1;
-    const long items = (long)((Pm.rows + NR - 1) / NR) * ((Pm.m + G::TT - 1) / G::TT);
+    const long items = (long)((Pm.rows + NRL - 1) / NRL) * ((Pm.m + G::TT - 1) / G::TT);
     long grid = (long)device_cu_count() * per_cu;
     if (grid > items) grid = items;
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, D, DEPTH, OCC>), dim3((unsigned)grid), dim3(GTHREADS), G::LDS, stream, Pm);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, D, DEPTH, OCC, NRL>), dim3((unsigned)grid), dim3(GTHREADS), G::LDS, stream,
+                       Pm);
     return hipGetLastError();
 }
 
 // Chunks per round: the largest power of two up to DMAX that divides the
 // K / 256 chunks of a row, so that every item is whole rounds.
-template <int MT, int DMAX, int OCC>
+template <int MT, int DMAX, int OCC, int NRL = 16>
 hipError_t launch_mt(const GemmParams &Pm, hipStream_t stream) {
     const int C = Pm.k / 256;
     if constexpr (DMAX >= 8) {
-        if (C % 8 == 0) return launch_geo<MT, 8, OCC>(Pm, stream);
+        if (C % 8 == 0) return launch_geo<MT, 8, OCC, NRL>(Pm, stream);
     }
     if constexpr (DMAX >= 4) {
-        if (C % 4 == 0) return launch_geo<MT, 4, OCC>(Pm, stream);
+        if (C % 4 == 0) return launch_geo<MT, 4, OCC, NRL>(Pm, stream);
     }
     if constexpr (DMAX >= 2) {
-        if (C % 2 == 0) return launch_geo<MT, 2, OCC>(Pm, stream);
+        if (C % 2 == 0) return launch_geo<MT, 2, OCC, NRL>(Pm, stream);
     }
-    return launch_geo<MT, 1, OCC>(Pm, stream);
+    return launch_geo<MT, 1, OCC, NRL>(Pm, stream);
 }
 
 #ifndef W4A8_GEMM_OCC
@@ -505,6 +509,11 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
     int mt = Pm.m <= 16 ? 1 : Pm.m <= 32 ? 2 : 4;
     const long wide_items = row_groups * ((Pm.m + 16 * mt - 1) / (16 * mt));
     if (mt > 1 && (wide_items < W4A8_GEMM_SPLIT_ITEMS || (mt == 4 && wide_items < 2 * W4A8_GEMM_SPLIT_ITEMS))) mt = 1;
+    // Long rows (K >= 8192: down) with fewer 16-row groups than CUs: 8-row
+    // items, eight chunks per round, one workgroup per CU. Down at M = 5..16
+    // takes 9.4-10.1 us against 10.3-10.4 with 16-row items (MI355X, rotated
+    // weights); at K = 2048 (o, q|k|v) 8-row items were slower.
+    if (mt == 1 && Pm.k >= 8192 && row_groups < device_cu_count()) return launch_mt<1, 8, 1, 8>(Pm, stream);
     if (mt == 1) return launch_mt<1, 8 / OCC, OCC>(Pm, stream);
     if (mt == 2) return launch_mt<2, 4 / OCC, OCC>(Pm, stream);
     return launch_mt<4, 2 / OCC, OCC>(Pm, stream);

@@ -248,7 +248,11 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       # the few-token GEMV (m = 2, or m <= 4 on large matrices):
                                       # ragged rows, one row, 48-chunk tiles (k = 6144), k = 8192
                                       (2, 1, 4096), (2, 300, 6144), (3, 8200, 2048), (4, 8197, 2048),
-                                      (4, 2048, 8192), (3, 1000, 8192), (2, 5, 8192)])
+                                      (4, 2048, 8192), (3, 1000, 8192), (2, 5, 8192),
+                                      # 8-row items (K >= 8192, fewer 16-row groups than CUs): the
+                                      # down shape, ragged rows, one item, several token groups
+                                      (8, 2048, 8192), (5, 1003, 8192), (16, 8, 8192), (12, 2050, 8192),
+                                      (33, 1001, 8192)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
@@ -262,7 +266,7 @@ def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
 
 
 @pytest.mark.parametrize("m,rows,k", [(24, 8200, 1024), (40, 2000, 1024), (2, 2000, 2048), (4, 8200, 2048),
-                                      (3, 600, 8192)])
+                                      (3, 600, 8192), (9, 1003, 8192)])
 def test_gemm_random_bytes(gpu, m, rows, k):
     """Arbitrary block bytes and activations (any finite fp16 scale) through both M > 1
     kernels (8,200 rows: the row-split one), row by row against the contract."""
