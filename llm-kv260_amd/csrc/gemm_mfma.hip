@@ -509,11 +509,14 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
     int mt = Pm.m <= 16 ? 1 : Pm.m <= 32 ? 2 : 4;
     const long wide_items = row_groups * ((Pm.m + 16 * mt - 1) / (16 * mt));
     if (mt > 1 && (wide_items < W4A8_GEMM_SPLIT_ITEMS || (mt == 4 && wide_items < 2 * W4A8_GEMM_SPLIT_ITEMS))) mt = 1;
-    // Long rows (K >= 8192: down) with fewer 16-row groups than CUs: 8-row
-    // items, eight chunks per round, one workgroup per CU. Down at M = 5..16
-    // takes 9.4-10.1 us against 10.3-10.4 with 16-row items (MI355X, rotated
-    // weights); at K = 2048 (o, q|k|v) 8-row items were slower.
-    if (mt == 1 && Pm.k >= 8192 && row_groups < device_cu_count()) return launch_mt<1, 8, 1, 8>(Pm, stream);
+    // One token group over long rows (K >= 8192: down) with fewer 16-row
+    // groups than CUs: 8-row items, eight chunks per round, one workgroup per
+    // CU. Down at M = 5..16 takes 9.2-10.1 us against 10.4-10.6 with 16-row
+    // items (MI355X, rotated weights). With several token groups (M > 16) a
+    // workgroup then runs its items one after another, 1.5-1.8x slower, and at
+    // K = 2048 (o, q|k|v) 8-row items were slower too.
+    if (mt == 1 && Pm.m <= 16 && Pm.k >= 8192 && row_groups < device_cu_count())
+        return launch_mt<1, 8, 1, 8>(Pm, stream);
     if (mt == 1) return launch_mt<1, 8 / OCC, OCC>(Pm, stream);
     if (mt == 2) return launch_mt<2, 4 / OCC, OCC>(Pm, stream);
     return launch_mt<4, 2 / OCC, OCC>(Pm, stream);
