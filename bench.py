@@ -439,17 +439,23 @@ CALL_COSTS = os.path.join(ROOT, "llm-kv260_amd", "caller", "call_costs")
 
 def run_call_costs():
     """Per-call costs through the reference ABI (the reference's bench_calls
-    table, docs/buildlog/evidence/0012-bench-calls.txt), in a process of its own."""
+    and bench_gemv2 tables, docs/buildlog/evidence/0012-bench-calls.txt and
+    0013-bench-gemv2.txt), in a process of its own."""
     import subprocess
-    env = dict(os.environ, KV260GEMV_UDMABUF_SIZES="udmabuf0=512M")
+    env = dict(os.environ, KV260GEMV_UDMABUF_SIZES="udmabuf0=1G")
     p = subprocess.run([CALL_COSTS, "--reps", "200"], capture_output=True, text=True, timeout=300, env=env)
     if p.returncode != 0:
         raise RuntimeError(f"call_costs failed: {p.stderr[-500:]}")
     out = json.loads(p.stdout.strip().splitlines()[-1])
-    out["reference_board"] = {"source": "docs/buildlog/evidence/0012-bench-calls.txt (KV260, one rank's shard)",
+    out["reference_board"] = {"source": "docs/buildlog/evidence/0012-bench-calls.txt and 0013-bench-gemv2.txt "
+                                        "(KV260, one rank's shard of four)",
                               "raw_best_us": {"tiny": 2.8, "x2048": 4.6, "x8192": 10.4},
                               "q8_us": {"k256": {"ref": 3.8, "neon": 1.0}, "k2048": {"ref": 30.3, "neon": 8.3},
-                                        "k8192": {"ref": 121.7, "neon": 33.5}}}
+                                        "k8192": {"ref": 121.7, "neon": 33.5}},
+                              "gemv2_cold_prefetched_us": {"qkv": [66.5, 30.9], "o": [53.9, 21.2],
+                                                           "gate_up": [348.1, 196.9], "down": [176.2, 77.1],
+                                                           "lm_head": [2816.8, 2658.1]},
+                              "token_65_calls_mac_ms": {"gap_0us": 13.35, "gap_300us": 8.14}}
     return out
 
 

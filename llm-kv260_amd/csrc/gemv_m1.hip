@@ -62,8 +62,10 @@ struct GemvParams {
     int rows;         // seg_rows * nseg
     int C;            // chunks per row, k / 256
     int rpw;          // rows per wave tile, 64 / C
-    int tiles;        // ceil(rows / rpw)
+    int tiles;        // ceil(rows / rpw); board layouts: nseg * tps
     int paired;       // v2 port layout
+    int tps;          // board layouts: tiles per segment
+    int prw;          // v2 port layout: row pairs per tile
     // Argmax epilogue (LM head): the first row of the largest y, written to
     // *argmax by the last workgroup to finish; the merged key and the ticket
     // counter live in the caller's workspace (both zero between calls).
@@ -125,22 +127,45 @@ struct BatchParams {
     BatchEntry e[W4A8_CHAIN_MAX_STEPS];
 };
 
-// Address of chunk c of row r (r counted over the whole matrix).
-template <bool PLAIN>
-__device__ __forceinline__ const uint8_t *chunk_ptr(const GemvParams &P, int r, int c) {
-    if constexpr (PLAIN) {
-        return P.seg[0] + ((size_t)r * (size_t)P.C + (size_t)c) * CHUNK_BYTES;
-    } else {
-        const int seg = r / P.seg_rows, local = r - seg * P.seg_rows;
-        const uint8_t *base = P.seg[seg];
-        if (P.paired) {
-            // v2 port region: row i pairs with row i + R/2; their 144-byte chunks alternate.
-            const int half = P.seg_rows >> 1;
-            const int which = local >= half, i = local - which * half;
-            return base + (((size_t)i * (size_t)P.C + (size_t)c) * 2 + (size_t)which) * CHUNK_BYTES;
-        }
-        return base + ((size_t)local * (size_t)P.C + (size_t)c) * CHUNK_BYTES;
+// Board layouts (four segments at separate addresses: the v1 quarters, or
+// the v2 port regions, where row i of a region pairs with row i + R/2 and
+// their 144-byte chunks alternate). Tiles are numbered segment by segment,
+// tps to a segment, so that none straddles two; a v2 tile takes prw whole
+// row pairs. Every tile is then one contiguous run of its segment, read with
+// the plain layout's coalesced, range-checked loads. A tile past the end
+// (segment index nseg or more) reads nothing.
+struct TileSpan {
+    const uint8_t *base;
+    uint32_t bytes;
+};
+
+__device__ __forceinline__ TileSpan board_tile(const GemvParams &P, int tile) {
+    const int t = __builtin_amdgcn_readfirstlane(tile);
+    const int seg = t / P.tps, lt = t - seg * P.tps;
+    TileSpan s{P.seg[0], 0u};
+    if (seg < P.nseg) {
+        const size_t row_bytes = (size_t)P.C * CHUNK_BYTES;
+        const size_t seg_bytes = (size_t)P.seg_rows * row_bytes;
+        const size_t tile_bytes = (size_t)(P.paired ? 2 * P.prw : P.rpw) * row_bytes;
+        const size_t off = (size_t)lt * tile_bytes;
+        s.base = P.seg[seg] + off;
+        s.bytes = (uint32_t)(seg_bytes - off < tile_bytes ? seg_bytes - off : tile_bytes);
     }
+    return s;
+}
+
+// Matrix row of row r of a board-layout tile (r < 2 prw for v2: pair r / 2,
+// its first row when r is even), or -1 when the tile has no such row.
+__device__ __forceinline__ int board_row(const GemvParams &P, int tile, int r) {
+    const int t = __builtin_amdgcn_readfirstlane(tile);
+    const int seg = t / P.tps, lt = t - seg * P.tps;
+    if (seg >= P.nseg) return -1;
+    if (P.paired) {
+        const int half = P.seg_rows >> 1, i = lt * P.prw + (r >> 1);
+        return (r >> 1) < P.prw && i < half ? seg * P.seg_rows + (r & 1) * half + i : -1;
+    }
+    const int local = lt * P.rpw + r;
+    return r < P.rpw && local < P.seg_rows ? seg * P.seg_rows + local : -1;
 }
 
 // Argmax workspace: the ticket counter and the merged key, each in its own 64-byte line.
@@ -156,31 +181,25 @@ struct Tile {
 };
 
 // Load the nine pieces of `tile` (lane l: bytes 1024 p + 16 l of the tile).
-// Plain layout: a tile past the end of the matrix reads nothing, and the
-// pieces of the last tile past the matrix's last byte read zeros (their terms
-// are never stored). Board layouts: per-lane addresses; a tile past the end
-// must not be asked for (the callers pass the wave's own first tile instead).
+// A tile past the end of the matrix reads nothing, and the pieces of the last
+// tile past the matrix's (or the segment's) last byte read zeros (their terms
+// are never stored).
 template <bool PLAIN>
-__device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lane, const int dr[9], const int col[9],
-                                          const int pc[9], Tile &t) {
+__device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lane, Tile &t) {
+    __amdgpu_buffer_rsrc_t tb;
     if constexpr (PLAIN) {
         const size_t tile_bytes = (size_t)P.rpw * (size_t)P.C * CHUNK_BYTES;
         const size_t total = (size_t)P.rows * (size_t)P.C * CHUNK_BYTES;
         const size_t off0 = (size_t)__builtin_amdgcn_readfirstlane(tile) * tile_bytes;
         const bool in = off0 < total;
         const uint32_t n = in ? (uint32_t)(total - off0 < (size_t)TILE_BYTES ? total - off0 : (size_t)TILE_BYTES) : 0u;
-        const __amdgpu_buffer_rsrc_t tb = buffer_of(P.seg[0] + (in ? off0 : 0), n);
-#pragma unroll
-        for (int p = 0; p < CHUNK_PIECES; ++p) t.p[p] = __builtin_amdgcn_raw_buffer_load_b128(tb, 1024 * p + 16 * lane, 0, CACHE_NT);
+        tb = buffer_of(P.seg[0] + (in ? off0 : 0), n);
     } else {
-        const int row0 = tile * P.rpw;
-#pragma unroll
-        for (int p = 0; p < CHUNK_PIECES; ++p) {
-            const int r = row0 + dr[p];
-            const uint8_t *g = (dr[p] < P.rpw && r < P.rows) ? chunk_ptr<false>(P, r, col[p]) + 16 * pc[p] : P.seg[0];
-            t.p[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(g));
-        }
+        const TileSpan sp = board_tile(P, tile);
+        tb = buffer_of(sp.base, sp.bytes);
     }
+#pragma unroll
+    for (int p = 0; p < CHUNK_PIECES; ++p) t.p[p] = __builtin_amdgcn_raw_buffer_load_b128(tb, 1024 * p + 16 * lane, 0, CACHE_NT);
 }
 
 // LDS layout (dynamic): per-wave slabs [waves][9216] | the staged activation
@@ -240,32 +259,20 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     uint32_t *s_x = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
 
     const int C = P.C, rpw = P.rpw;
-    const int my_r = lane / C;
-    const int my_c = lane - my_r * C;
-    const bool lane_live = my_r < rpw;
-
-    // Piece 64 p + lane of a tile: chunk q = n / 9 of the tile, piece n % 9
-    // of the chunk; the chunk is row q / C (of the tile), column q % C.
-    int dr[9], col[9], pc[9];
-    if constexpr (!PLAIN) {
-#pragma unroll
-        for (int p = 0; p < CHUNK_PIECES; ++p) {
-            const int n = 64 * p + lane, q = n / CHUNK_PIECES;
-            pc[p] = n - q * CHUNK_PIECES;
-            dr[p] = q / C;
-            col[p] = q - dr[p] * C;
-        }
-    }
+    // Lane l takes chunk l of the tile: row l / C, column l % C; in a v2
+    // tile the chunks of a row pair alternate, so chunk l is column
+    // (l / 2) % C of row 2 (l / 2C) + l % 2 of the tile.
+    const bool paired = !PLAIN && P.paired;
+    const int pq = paired ? lane >> 1 : lane;
+    const int my_c = pq - (pq / C) * C;
+    const bool lane_live = paired ? lane < 2 * P.prw * C : lane / C < rpw;
+    // Rows per tile as the ordered sums see them.
+    const int trows = paired ? 2 * P.prw : rpw;
 
     constexpr int DEPTH = depth_of<PLAIN>();
     int tile = block * waves + wave;
     const int tstride = nblocks * waves;
     const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
-    // Board layouts: loads past the wave's last tile (the refills of its last
-    // round) read its first tile again, lines it already fetched, never a
-    // line every wave would hammer at once; their data is never used. (The
-    // plain layout's out-of-range loads read nothing at all.)
-    const int home = tile < P.tiles ? tile : 0;
 
     // 1. The activation. Its loads go out before any weight tile's; the
     // staging below waits for them only.
@@ -351,10 +358,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                 w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
             }
         }
-        if constexpr (decltype(refill)::value) {
-            const int tn = tile + DEPTH * tstride;
-            load_tile<PLAIN>(P, PLAIN || tn < P.tiles ? tn : home, lane, dr, col, pc, b);
-        }
+        if constexpr (decltype(refill)::value) load_tile<PLAIN>(P, tile + DEPTH * tstride, lane, b);
         float t[8];
         chunk_terms(w, xv, xd, xs, t);
         wave_sync_lds();
@@ -366,7 +370,12 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         wave_sync_lds();
         // Accumulator a of row r: term a of chunks 0 .. C-1, in order, from
         // +0.0f. Eight rows per pass (more than one pass only when C < 8).
-        auto lane_sum = [&](int r) { return ordered_lane_sum(s_t, r, rpw, C, acc_a); };
+        // Row r of a v2 tile has its chunks at 2 (r / 2) C + r % 2 + 2 c.
+        auto lane_sum = [&](int r) {
+            if (paired) return ordered_lane_sum_at(s_t, 2 * (r >> 1) * C + (r & 1), 2, r < trows, C, acc_a);
+            return ordered_lane_sum(s_t, r, rpw, C, acc_a);
+        };
+        auto row_of = [&](int r) { return PLAIN ? (r < rpw && tile * rpw + r < P.rows ? tile * rpw + r : -1) : board_row(P, tile, r); };
         if constexpr (PAIR) {
             // Both halves issue one store; the gate's goes out of range.
             const float yv = tree8_dpp(lane_sum(acc_r));
@@ -378,17 +387,17 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             store_y(y_rsrc, up && mine ? 4 * (row - (P.rows >> 1)) : OUT_OF_RANGE, act);
         } else if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
-            const int row = tile * rpw + acc_r;
-            const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
+            const int row = row_of(acc_r);
+            const bool mine = acc_a == 0 && row >= 0;
             store_y(y_rsrc, mine ? 4 * row : OUT_OF_RANGE, yv);
             if constexpr (ARGMAX) {
                 if (mine) best = max_u64(best, argmax_key(yv, row));
             }
         } else {
-            for (int r = acc_r; r - acc_r < rpw; r += 8) {
+            for (int r = acc_r; r - acc_r < trows; r += 8) {
                 const float yv = tree8_dpp(lane_sum(r));
-                const int row = tile * rpw + r;
-                if (r < rpw && acc_a == 0 && row < P.rows) {
+                const int row = row_of(r);
+                if (acc_a == 0 && row >= 0) {
                     P.y[row] = yv;
                     if constexpr (ARGMAX) best = max_u64(best, argmax_key(yv, row));
                 }
@@ -406,10 +415,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     if (n_my >= 2) {
         Tile buf[DEPTH];
 #pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            const int t = tile + d * tstride;
-            load_tile<PLAIN>(P, PLAIN || t < P.tiles ? t : home, lane, dr, col, pc, buf[d]);
-        }
+        for (int d = 0; d < DEPTH; ++d) load_tile<PLAIN>(P, tile + d * tstride, lane, buf[d]);
         stage_x();
         int done = 0;
         for (; done + DEPTH <= n_my; done += DEPTH) {
@@ -421,7 +427,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             if (done + d < n_my) step(buf[d], last_t{});
     } else if (n_my == 1) {
         Tile b;
-        load_tile<PLAIN>(P, tile, lane, dr, col, pc, b);
+        load_tile<PLAIN>(P, tile, lane, b);
         stage_x();
         step(b, last_t{});
     } else {
@@ -561,8 +567,19 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     if (P.C < 1 || P.C > 64 || w.k % 256) return hipErrorInvalidValue;
     P.rpw = 64 / P.C;
     P.tiles = (P.rows + P.rpw - 1) / P.rpw;
-    if (P.tiles < 1) return hipSuccess;
     const bool plain = w.nseg == 1 && !w.paired;
+    if (!plain) {
+        // Board layouts: whole tiles per segment (v2: whole row pairs).
+        if (w.paired) {
+            if (w.seg_rows % 2 || P.rpw < 2) return hipErrorInvalidValue;
+            P.prw = P.rpw / 2;
+            P.tps = (w.seg_rows / 2 + P.prw - 1) / P.prw;
+        } else {
+            P.tps = (w.seg_rows + P.rpw - 1) / P.rpw;
+        }
+        P.tiles = w.nseg * P.tps;
+    }
+    if (P.tiles < 1) return hipSuccess;
     const int cus = device_cu_count();
     const int nb = w.k / QK;
     // Staged activation: int8 values, fp32 scale and int32 sum per block; for

@@ -247,4 +247,23 @@ __device__ __forceinline__ float ordered_lane_sum(const float *s_t, int r, int r
     return acc;
 }
 
+// The same with the row's chunks at positions start + cstride c of the
+// slab (a v2 tile's rows: their chunks alternate with the paired row's).
+__device__ __forceinline__ float ordered_lane_sum_at(const float *s_t, int start, int cstride, bool live, int C,
+                                                     int acc_a) {
+    float acc = 0.0f;
+    if (live) {
+        const float *src = s_t + start * 9 + acc_a;
+        const int step = 9 * cstride;
+        for (int c0 = 0; c0 < C; c0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = c0 + j < C ? src[step * (c0 + j)] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = acc + v[j];
+        }
+    }
+    return acc;
+}
+
 }  // namespace w4a8
