@@ -749,6 +749,9 @@ def main() -> int:
         "cpu_baseline": cpu,
     })
     print(json.dumps(out), flush=True)
+    if not verified:
+        log("a timed output differs from the oracle's digest (see \"verification\")")
+        return 1
     return 0
 
 
