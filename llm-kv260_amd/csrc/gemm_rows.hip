@@ -87,9 +87,12 @@ struct RGeo {
     static constexpr int SD = (D_PIECES + RTHREADS - 1) / RTHREADS;
 };
 
-template <int MT>
+// PK > 1 (one token tile, M <= 16 / PK): PK blocks share one MFMA result
+// tile (packed_group), so that the fp32 epilogue touches only live outputs.
+template <int MT, int PK = 1>
 struct RowsKernel {
     using G = RGeo<MT>;
+    static_assert(PK == 1 || (MT == 1 && (PK == 2 || PK == 4)), "blocks per tile: 2 or 4, one token tile");
 
     struct Regs {
         u32x4 w[SW];
@@ -178,10 +181,12 @@ struct RowsKernel {
             }
     }
 
-    // Block B (0..15) of the segment: its MFMA sums for every token tile.
+    // Block B (0..15) of the segment, row j of the pair's group: the MFMA
+    // weight operand of lane group g (the nibbles of weights 8g .. 8g + 7:
+    // the low nibbles of bytes 0..7, g = 0, and 8..15, g = 1, then the high
+    // nibbles, g = 2, 3) and the block's scale.
     template <int B>
-    static __device__ __forceinline__ void block_sums(const uint8_t *slab, const uint8_t *xbuf, int j, int g, v4i v[MT],
-                                                      float &dw, float dx[MT]) {
+    static __device__ __forceinline__ void weights_of(const uint8_t *slab, int j, int g, long &bw, float &dw) {
         const int h = g & 1;
         const int shift = (g >> 1) * 4;
         const uint8_t *wrow = slab + j * WPITCH + 18 * B;
@@ -200,9 +205,17 @@ struct RowsKernel {
             hi = run[1];
             d_bits = *reinterpret_cast<const uint32_t *>(wrow - 2) >> 16;
         }
-        const long bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
-        const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
+        bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
         dw = half_bits_to_float(d_bits);
+    }
+
+    // Block B (0..15) of the segment: its MFMA sums for every token tile.
+    template <int B>
+    static __device__ __forceinline__ void block_sums(const uint8_t *slab, const uint8_t *xbuf, int j, int g, v4i v[MT],
+                                                      float &dw, float dx[MT]) {
+        long bw;
+        weights_of<B>(slab, j, g, bw, dw);
+        const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
         const uint8_t *xa = xbuf + j * G::APITCH + 32 * B + 8 * g;
         const float *xs = reinterpret_cast<const float *>(xbuf + G::XD_OFF) + B * G::XDP + 4 * g + (j & 3);
 #pragma unroll
@@ -241,13 +254,64 @@ struct RowsKernel {
             }
     }
 
+    // Packed tiles (PK blocks of at most TPB = 16 / PK tokens each): the A
+    // operand's 16 rows are (block c, token t) = (i / TPB, i % TPB). Block c's
+    // MFMA sees zeros in every other block's rows, so the PK MFMAs put each
+    // block's exact int32 sums in its own rows of one tile; one more MFMA
+    // against -8 adds -8 sum(x) to every row. The result's lane l then holds
+    // block c = 4 (l / 16) / TPB of the group, tokens 4 (l / 16) % TPB + r
+    // (r = 0..3), row l % 16: every lane live, one fp32 term per value.
+    template <int B0, int C>
+    static __device__ __forceinline__ void packed_mfma(const uint8_t *slab, int j, int g, int ablk, int dblk, long ax,
+                                                       v4i &d, float &dw) {
+        long bw;
+        float dwc;
+        weights_of<B0 + C>(slab, j, g, bw, dwc);
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ablk == C ? ax : 0L, bw, d, 0, 0, 0);
+        dw = dblk == C ? dwc : dw;
+        if constexpr (C + 1 < PK) packed_mfma<B0, C + 1>(slab, j, g, ablk, dblk, ax, d, dw);
+    }
+
+    // Blocks B0 .. B0 + PK - 1: their terms, added to the lane's accumulator
+    // (that of its block, B0 % 8 + c) in block order.
+    template <int B0>
+    static __device__ __forceinline__ void packed_group(const uint8_t *slab, const uint8_t *xbuf, int j, int g,
+                                                        float acc[4]) {
+        constexpr int TPB = 16 / PK;
+        const int ablk = j / TPB, atok = j - ablk * TPB;          // this lane's A row (block, token)
+        const int dblk = 4 * g / TPB, dtok = 4 * g - dblk * TPB;  // its result rows
+        const long ax = *reinterpret_cast<const long *>(xbuf + atok * G::APITCH + 32 * (B0 + ablk) + 8 * g);
+        v4i d = {0, 0, 0, 0};
+        float dw = 0.0f;
+        packed_mfma<B0, 0>(slab, j, g, ablk, dblk, ax, d, dw);
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, as_long(0xF8F8F8F8u, 0xF8F8F8F8u), d, 0, 0, 0);
+        // The four tokens' scales of the lane's block: one 16-byte read (a
+        // block's scales are a row of XDP floats, tokens along it).
+        const float *xs = reinterpret_cast<const float *>(xbuf + G::XD_OFF) + (B0 + dblk) * G::XDP + dtok;
+        const float4 dx = *reinterpret_cast<const float4 *>(xs);
+        const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float a = (float)d[r] * dw;
+            acc[r] = acc[r] + a * dxs[r];
+        }
+    }
+
     // The wave's eight blocks of a segment: its four accumulators' blocks
     // 4 half + c, then 8 + 4 half + c, in order. Two blocks per phase at four
     // token tiles keeps the MFMA results within the register budget.
     template <int H>
     static __device__ __forceinline__ void segment(const uint8_t *slab, const uint8_t *xbuf, int j, int g,
                                                    float acc[4][MT][4]) {
-        if constexpr (MT <= 2) {
+        if constexpr (PK == 4) {
+            packed_group<4 * H>(slab, xbuf, j, g, acc[0][0]);
+            packed_group<8 + 4 * H>(slab, xbuf, j, g, acc[0][0]);
+        } else if constexpr (PK == 2) {
+            packed_group<4 * H>(slab, xbuf, j, g, acc[0][0]);
+            packed_group<4 * H + 2>(slab, xbuf, j, g, acc[1][0]);
+            packed_group<8 + 4 * H>(slab, xbuf, j, g, acc[0][0]);
+            packed_group<8 + 4 * H + 2>(slab, xbuf, j, g, acc[1][0]);
+        } else if constexpr (MT <= 2) {
             blocks<4 * H, 4>(slab, xbuf, j, g, acc);
             blocks<8 + 4 * H, 4>(slab, xbuf, j, g, acc);
         } else {
@@ -313,8 +377,49 @@ struct RowsKernel {
             }
         }
 
-        // The pair meets: wave 1 hands (a4 + a5) + (a6 + a7) to wave 0.
         float *ex = reinterpret_cast<float *>(lds + G::EX_OFF) + pair * G::TT * 16;
+        if constexpr (PK > 1) {
+            // The wave's four accumulators of an output sit in lanes 16 apart
+            // (PK = 4: acc[0] of lane groups 0..3 hold a0..a3) or 32 apart in
+            // two arrays (PK = 2: acc[0] holds a0 / a1, acc[1] a2 / a3): the
+            // tree's (a0 + a1) + (a2 + a3), then the pair's last add through
+            // LDS as below. Lanes of result block 0 hold the sums.
+            constexpr int TPB = 16 / PK;
+            const int dblk = 4 * g / TPB, dtok = 4 * g - dblk * TPB;
+            float part[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (PK == 4) {
+                    const float s = acc[0][0][r] + __shfl_xor(acc[0][0][r], 16);
+                    part[r] = s + __shfl_xor(s, 32);
+                } else {
+                    const float s01 = acc[0][0][r] + __shfl_xor(acc[0][0][r], 32);
+                    const float s23 = acc[1][0][r] + __shfl_xor(acc[1][0][r], 32);
+                    part[r] = s01 + s23;
+                }
+            }
+            if (half == 1 && dblk == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ex[(dtok + r) * 16 + j] = part[r];
+            }
+            __syncthreads();
+            if (half == 0) {
+                const uint32_t y_bytes = (uint32_t)P.m * (uint32_t)P.rows * 4u;
+                const __amdgpu_buffer_rsrc_t yb = rsrc(P.y, y_bytes);
+                const bool row_ok = n0 + j < P.rows && dblk == 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tok = dtok + r;
+                    const float yv = part[r] + ex[tok * 16 + j];
+                    const bool ok = row_ok && tok < P.m;
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(yv), yb, ok ? (int)(((uint32_t)tok * (uint32_t)P.rows + (uint32_t)(n0 + j)) * 4u) : OUT_OF_RANGE,
+                        0, 0);
+                }
+            }
+            return;
+        }
+        // The pair meets: wave 1 hands (a4 + a5) + (a6 + a7) to wave 0.
         float part[MT][4];
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -346,19 +451,19 @@ struct RowsKernel {
     }
 };
 
-template <int MT>
+template <int MT, int PK>
 __global__ __launch_bounds__(RTHREADS) void gemm_rows_kernel(RowsParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    RowsKernel<MT>::run(P, lds);
+    RowsKernel<MT, PK>::run(P, lds);
 }
 
-template <int MT>
+template <int MT, int PK = 1>
 hipError_t launch_rows_mt(const RowsParams &P, hipStream_t stream) {
-    const void *fn = reinterpret_cast<const void *>(&gemm_rows_kernel<MT>);
+    const void *fn = reinterpret_cast<const void *>(&gemm_rows_kernel<MT, PK>);
     const hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
     if (e != hipSuccess) return e;
     const int grid = (P.rows + 16 * PAIRS - 1) / (16 * PAIRS);
-    hipLaunchKernelGGL(gemm_rows_kernel<MT>, dim3((unsigned)grid), dim3(RTHREADS), RGeo<MT>::LDS, stream, P);
+    hipLaunchKernelGGL((gemm_rows_kernel<MT, PK>), dim3((unsigned)grid), dim3(RTHREADS), RGeo<MT>::LDS, stream, P);
     return hipGetLastError();
 }
 
@@ -379,6 +484,13 @@ hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y,
     P.k = k;
     P.m = m;
     P.x_stride = k + k / 8;
+#ifndef W4A8_ROWS_PACKED
+#define W4A8_ROWS_PACKED 1
+#endif
+#if W4A8_ROWS_PACKED
+    if (m <= 4) return launch_rows_mt<1, 4>(P, stream);
+    if (m <= 8) return launch_rows_mt<1, 2>(P, stream);
+#endif
     if (m <= 16) return launch_rows_mt<1>(P, stream);
     if (m <= 32) return launch_rows_mt<2>(P, stream);
     return launch_rows_mt<4>(P, stream);

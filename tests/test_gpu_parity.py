@@ -252,7 +252,12 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       # 8-row items (K >= 8192, fewer 16-row groups than CUs): the
                                       # down shape, ragged rows, one item, several token groups
                                       (8, 2048, 8192), (5, 1003, 8192), (16, 8, 8192), (12, 2050, 8192),
-                                      (33, 1001, 8192)])
+                                      (33, 1001, 8192),
+                                      # the row-split kernel's packed tiles: 2 blocks x 8 tokens (m = 5..8)
+                                      # and 4 blocks x 4 tokens (m <= 4 where the few-token GEMV does not
+                                      # take the shape); ragged rows, 1-3 K segments
+                                      (5, 8200, 2048), (8, 8256, 4096), (7, 9000, 1536), (6, 8192, 512),
+                                      (4, 8200, 12288), (2, 8193, 1024), (69, 8200, 1024)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
@@ -266,7 +271,7 @@ def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
 
 
 @pytest.mark.parametrize("m,rows,k", [(24, 8200, 1024), (40, 2000, 1024), (2, 2000, 2048), (4, 8200, 2048),
-                                      (3, 600, 8192), (9, 1003, 8192)])
+                                      (3, 600, 8192), (9, 1003, 8192), (7, 8200, 2048), (3, 8200, 512)])
 def test_gemm_random_bytes(gpu, m, rows, k):
     """Arbitrary block bytes and activations (any finite fp16 scale) through both M > 1
     kernels (8,200 rows: the row-split one), row by row against the contract."""
