@@ -7,8 +7,8 @@
 // with b % 8 in that range, in increasing b, and adds each term to accumulator
 // b % 8 from +0.0f. At the end the pair meets once: wave 0's
 // (a0 + a1) + (a2 + a3) plus wave 1's (a4 + a5) + (a6 + a7) is the
-// adjacent-pair tree's last add. A workgroup holds four pairs (64 rows), so a
-// matrix of N rows has N / 64 workgroups and every wave has the same work.
+// adjacent-pair tree's last add. A workgroup holds two or four pairs (32 or
+// 64 rows, pairs_of), so every wave has the same work.
 //
 // K goes by segments of 512 values (16 blocks). Per segment a pair stages its
 // 16 rows' 288-byte runs in a slab of its own, and the workgroup stages the
@@ -31,11 +31,13 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-#ifndef W4A8_ROWS_PAIRS
-#define W4A8_ROWS_PAIRS 4
-#endif
-constexpr int PAIRS = W4A8_ROWS_PAIRS;            // 16-row groups per workgroup
-constexpr int RTHREADS = 64 * 2 * PAIRS;
+// 16-row groups (pairs of waves) per workgroup: two at one token tile (two
+// workgroups then share a CU, each running while the other waits at its
+// segment barrier: the LM head at M = 9..16 in 51-53 us against 67-70 with
+// four), four at two or four token tiles (whose workgroups fill the CU's
+// registers alone; two pairs were 1.1-1.6x slower there).
+template <int MT>
+constexpr int pairs_of() { return MT == 1 ? 2 : 4; }
 constexpr int SEG = 512;                          // activation values per segment
 constexpr int SEG_BLOCKS = SEG / QK;              // 16
 constexpr int SEG_ROW_BYTES = SEG_BLOCKS * Q4_0_BYTES;   // 288
@@ -77,14 +79,16 @@ struct RGeo {
     static constexpr int XDP = TT + 4;                       // scale rows: [16 blocks][XDP]
     static constexpr int XD_OFF = TT * APITCH;
     static constexpr int XBUF = XD_OFF + SEG_BLOCKS * XDP * 4;
+    static constexpr int PAIRS = pairs_of<MT>();
+    static constexpr int THREADS = 64 * 2 * PAIRS;
     static constexpr int SLAB_OFF = 2 * XBUF;                // [2][PAIRS] slabs
     static constexpr int EX_OFF = SLAB_OFF + 2 * PAIRS * SLAB;   // pair exchange [PAIRS][TT][16] floats
     static constexpr int LDS = EX_OFF + PAIRS * TT * 16 * 4;
     static_assert(LDS <= LDS_MAX, "LDS budget");
     static constexpr int X_PIECES = TT * (SEG / 16);         // int8 pieces per segment
     static constexpr int D_PIECES = TT * (SEG_BLOCKS / 4);   // scale pieces (4 scales each)
-    static constexpr int SX = (X_PIECES + RTHREADS - 1) / RTHREADS;
-    static constexpr int SD = (D_PIECES + RTHREADS - 1) / RTHREADS;
+    static constexpr int SX = (X_PIECES + THREADS - 1) / THREADS;
+    static constexpr int SD = (D_PIECES + THREADS - 1) / THREADS;
 };
 
 // PK > 1 (one token tile, M <= 16 / PK): PK blocks share one MFMA result
@@ -124,7 +128,7 @@ struct RowsKernel {
         }
 #pragma unroll
         for (int i = 0; i < G::SX; ++i) {
-            const int n = tid + RTHREADS * i;
+            const int n = tid + G::THREADS * i;
             const int t = n / 32, p = n - 32 * t;
             const bool has = n < G::X_PIECES;
             s.x_go[i] = has ? (uint32_t)t * (uint32_t)P.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
@@ -132,7 +136,7 @@ struct RowsKernel {
         }
 #pragma unroll
         for (int i = 0; i < G::SD; ++i) {
-            const int n = tid + RTHREADS * i;
+            const int n = tid + G::THREADS * i;
             const int p = n / G::TT, t = n - G::TT * p;   // tokens fastest: the transposing writes spread over banks
             const bool has = n < G::D_PIECES;
             s.d_go[i] = has ? (uint32_t)t * (uint32_t)P.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
@@ -167,11 +171,11 @@ struct RowsKernel {
             if (s.w_lo[i] >= 0) *reinterpret_cast<u32x4 *>(slab + s.w_lo[i]) = rg.w[i];
 #pragma unroll
         for (int i = 0; i < G::SX; ++i)
-            if ((i + 1) * RTHREADS <= G::X_PIECES || s.x_lo[i] >= 0)
+            if ((i + 1) * G::THREADS <= G::X_PIECES || s.x_lo[i] >= 0)
                 *reinterpret_cast<u32x4 *>(xbuf + s.x_lo[i]) = rg.x[i];
 #pragma unroll
         for (int i = 0; i < G::SD; ++i)
-            if ((i + 1) * RTHREADS <= G::D_PIECES || s.d_lo[i] >= 0) {
+            if ((i + 1) * G::THREADS <= G::D_PIECES || s.d_lo[i] >= 0) {
                 uint32_t *xd = reinterpret_cast<uint32_t *>(xbuf) + s.d_lo[i];
                 const u32x4 v = rg.d[i];
                 xd[0] = v.x;
@@ -331,7 +335,7 @@ struct RowsKernel {
         const int j = lane & 15, g = lane >> 4;
         const int row_bytes = P.k / QK * Q4_0_BYTES;
         const int nseg = P.k / SEG;
-        const int n0 = ((int)blockIdx.x * PAIRS + pair) * 16;   // the pair's first row
+        const int n0 = ((int)blockIdx.x * G::PAIRS + pair) * 16;   // the pair's first row
 
         Slots s;
         slots(P, row_bytes, s);
@@ -360,7 +364,7 @@ struct RowsKernel {
                 const int sg = sg0 + d;
                 if (sg < nseg) {
                     const uint8_t *xbuf = lds + (sg & 1) * G::XBUF;
-                    const uint8_t *slab = lds + G::SLAB_OFF + ((sg & 1) * PAIRS + pair) * SLAB;
+                    const uint8_t *slab = lds + G::SLAB_OFF + ((sg & 1) * G::PAIRS + pair) * SLAB;
                     if (half == 0)
                         segment<0>(slab, xbuf, j, g, acc);
                     else
@@ -370,7 +374,7 @@ struct RowsKernel {
                 // segment sg - 1, before the previous barrier); its registers
                 // then take segment sg + 1 + DEPTH.
                 const int nx = sg + 1;
-                stage(lds + (nx & 1) * G::XBUF, lds + G::SLAB_OFF + ((nx & 1) * PAIRS + pair) * SLAB, s,
+                stage(lds + (nx & 1) * G::XBUF, lds + G::SLAB_OFF + ((nx & 1) * G::PAIRS + pair) * SLAB, s,
                       rg[(d + 1) % DEPTH]);
                 load(P, s, row_bytes, n0, nx + DEPTH, nseg, rg[(d + 1) % DEPTH]);
                 __syncthreads();
@@ -452,7 +456,7 @@ struct RowsKernel {
 };
 
 template <int MT, int PK>
-__global__ __launch_bounds__(RTHREADS) void gemm_rows_kernel(RowsParams P) {
+__global__ __launch_bounds__(64 * 2 * pairs_of<MT>()) void gemm_rows_kernel(RowsParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     RowsKernel<MT, PK>::run(P, lds);
 }
@@ -462,8 +466,9 @@ hipError_t launch_rows_mt(const RowsParams &P, hipStream_t stream) {
     const void *fn = reinterpret_cast<const void *>(&gemm_rows_kernel<MT, PK>);
     const hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
     if (e != hipSuccess) return e;
-    const int grid = (P.rows + 16 * PAIRS - 1) / (16 * PAIRS);
-    hipLaunchKernelGGL((gemm_rows_kernel<MT, PK>), dim3((unsigned)grid), dim3(RTHREADS), RGeo<MT>::LDS, stream, P);
+    using G = RGeo<MT>;
+    const int grid = (P.rows + 16 * G::PAIRS - 1) / (16 * G::PAIRS);
+    hipLaunchKernelGGL((gemm_rows_kernel<MT, PK>), dim3((unsigned)grid), dim3(G::THREADS), G::LDS, stream, P);
     return hipGetLastError();
 }
 
