@@ -102,7 +102,10 @@ def _case(rows, k, seed):
     return blocks, C.pack_x_for_engine(xq, xd), C.gemv_q4_0(blocks, k, xq, xd)
 
 
-@pytest.mark.parametrize("rows,k", [(512, 2048), (64, 8192), (2048, 2048)])
+@pytest.mark.parametrize("rows,k", [(512, 2048), (64, 8192), (2048, 2048),
+                                    # rows per tile that do not divide a quarter (k = 768: 21 rows per
+                                    # tile; k = 1280: 12; k = 6144: 2), quarters shorter than a tile
+                                    (48, 768), (208, 1280), (1040, 6144), (16, 256)])
 def test_v1_quarters_and_run(board, rows, k):
     """gemv_dev_start4 over quarters at staggered pool addresses (tp_llama.cpp:105-119),
     then gemv_dev_run over the same rows contiguous."""
@@ -139,7 +142,10 @@ def _chunk_offset(r, c, rows, k):
     return ((pair * chunks + c) * 2 + second) * 144, r // per_port
 
 
-@pytest.mark.parametrize("rows,k", [(768, 2048), (32, 256), (2048, 8192), (4096, 2048)])
+@pytest.mark.parametrize("rows,k", [(768, 2048), (32, 256), (2048, 8192), (4096, 2048),
+                                    # odd chunks per row: tiles of 10 (k = 768), 6 (k = 1280) and 1
+                                    # (k = 6144) row pairs, port regions that end inside a tile
+                                    (96, 768), (160, 1280), (544, 6144), (352, 3840)])
 def test_v2_fetch_then_mac(board, rows, k):
     """gemv2_fetch_start + gemv2_mac_start + gemv2_mac_wait on the chunk-interleaved
     layout, as engine_t::gemv issues them (tp_llama.cpp:364-368)."""
