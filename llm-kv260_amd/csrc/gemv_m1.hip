@@ -170,9 +170,8 @@ __device__ __forceinline__ int board_row(const GemvParams &P, int tile, int r) {
 
 // Argmax workspace: the ticket counter and the merged key, each in its own 64-byte line.
 constexpr size_t ARGMAX_KEY_OFFSET = 64;
-// Tiles per wave held in registers. Two: a third (tried for plain matrices)
-// raised no shape's rate and took 36 VGPRs, and the board layouts' per-lane
-// address tables need those registers anyway.
+// Tiles per wave held in registers. Two: a third raised no shape's rate and
+// took 36 VGPRs.
 template <bool PLAIN>
 constexpr int depth_of() { return 2; }
 
