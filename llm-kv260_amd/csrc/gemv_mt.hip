@@ -82,7 +82,9 @@ __device__ __forceinline__ int32_t block_dot_with_sum(const uint32_t qs[4], uint
 
 // PASSES: staging rounds of blocks per thread, m * nb <= PASSES * threads.
 // TG: tokens computed per round of ordered sums.
-template <int PASSES, int TG>
+// SHARED_SUMS: a tile's rows take at most 32 lanes per token (K >= 4096), so
+// the ordered sums of several tokens share one pass (otherwise one per token).
+template <int PASSES, int TG, bool SHARED_SUMS>
 __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -175,12 +177,32 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
 #pragma unroll
                 for (int j = 0; j < 8; ++j) s_t[u * 576 + 9 * lane + j] = term[u][j];
             wave_sync_lds();
+            // Ordered sums. A tile's rows take 8 rpw lanes per token: all 64
+            // at K = 2048, one token at a time; 16 at K = 8192, where lane
+            // (u, r, a) takes accumulator a of row r of token u0 + u and one
+            // pass serves four tokens, their dependent adds side by side
+            // (down at M = 3, 4: 6.8-7.0 us against 7.5-7.6 one token at a
+            // time).
+            if constexpr (!SHARED_SUMS) {
 #pragma unroll
-            for (int u = 0; u < TG; ++u) {
-                const float yv = tree8_dpp(ordered_lane_sum(s_t + u * 576, acc_r, rpw, C, acc_a));
-                const bool store = mine && t0 + u < P.m;
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), y_rsrc,
-                                                      store ? 4 * ((t0 + u) * P.rows + row) : OUT_OF_RANGE, 0, 0);
+                for (int u = 0; u < TG; ++u) {
+                    const float yv = tree8_dpp(ordered_lane_sum(s_t + u * 576, acc_r, rpw, C, acc_a));
+                    const bool store = mine && t0 + u < P.m;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), y_rsrc,
+                                                          store ? 4 * ((t0 + u) * P.rows + row) : OUT_OF_RANGE, 0, 0);
+                }
+            } else {
+                const int per_tok = 8 * rpw, tok_pass = 64 / per_tok;
+                const int sum_u = lane / per_tok, sum_r = (lane - sum_u * per_tok) >> 3;
+                const int srow = tile * rpw + sum_r;
+                for (int u0 = 0; u0 < TG; u0 += tok_pass) {
+                    const int u = u0 + sum_u;
+                    const bool live = sum_u < tok_pass && u < TG;
+                    const float yv = tree8_dpp(ordered_lane_sum(s_t + (live ? u : u0) * 576, sum_r, rpw, C, acc_a));
+                    const bool store = live && acc_a == 0 && sum_r < rpw && srow < P.rows && t0 + u < P.m;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), y_rsrc,
+                                                          store ? 4 * ((t0 + u) * P.rows + srow) : OUT_OF_RANGE, 0, 0);
+                }
             }
         }
         wave_sync_lds();
@@ -210,10 +232,10 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
     }
 }
 
-template <int PASSES, int TG>
+template <int PASSES, int TG, bool SHARED_SUMS>
 __global__ __launch_bounds__(MT_THREADS) void gemv_mt_kernel(MtParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    gemv_mt_body<PASSES, TG>(P, blockIdx.x, gridDim.x, lds);
+    gemv_mt_body<PASSES, TG, SHARED_SUMS>(P, blockIdx.x, gridDim.x, lds);
 }
 
 template <int PASSES>
@@ -224,8 +246,13 @@ hipError_t launch_mt_pass(const MtParams &P, int grid, int threads, size_t lds, 
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), lds, stream, P);
         return hipGetLastError();
     };
-    if (P.m <= 2) return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 2>), gemv_mt_kernel<PASSES, 2>);
-    return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 4>), gemv_mt_kernel<PASSES, 4>);
+    if (P.rpw <= 4) {
+        if (P.m <= 2)
+            return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 2, true>), gemv_mt_kernel<PASSES, 2, true>);
+        return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 4, true>), gemv_mt_kernel<PASSES, 4, true>);
+    }
+    if (P.m <= 2) return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 2, false>), gemv_mt_kernel<PASSES, 2, false>);
+    return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 4, false>), gemv_mt_kernel<PASSES, 4, false>);
 }
 
 }  // namespace
