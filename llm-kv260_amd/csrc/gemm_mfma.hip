@@ -533,15 +533,12 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hipStream_t stream) {
     // One token is the M = 1 GEMV, byte for byte by the contract, and faster.
     // A few tokens are its weight stream with the arithmetic per token
-    // (gemv_mt.hip), where that is the faster (MI355X, rotated weights):
-    // m = 2 everywhere (gate|up 6.7 against 9.5 us, down 5.7 against 10.3,
-    // q|k|v 4.4 against 5.0), and m = 3, 4 on the large matrices (gate|up 8.2
-    // against 9.7 us, down 7.6 against 10.4), where the MFMA kernels' rounds
-    // cost more than the per-token arithmetic; past that the arithmetic (0.8 us
-    // per token on gate|up) loses to the MFMA kernels.
+    // (gemv_mt.hip), up to the m where that is the faster (gemv_mt_max_m:
+    // 2 to 6 by shape), where the MFMA kernels' rounds cost more than the
+    // per-token arithmetic; past that the arithmetic (0.8 us per token on
+    // gate|up) loses to the MFMA kernels.
     if (m == 1) return launch_gemv_m1(w, x, X_ENGINE, y, stream);
-    const bool large = w.rows >= 8192 || w.k >= 8192;
-    if (w.nseg == 1 && !w.paired && (m == 2 || (m <= 4 && large)) && gemv_mt_fits(m, w.rows, w.k))
+    if (w.nseg == 1 && !w.paired && m <= gemv_mt_max_m(w.rows, w.k) && gemv_mt_fits(m, w.rows, w.k))
         return launch_gemv_mt(w.seg[0], x, m, y, w.rows, w.k, stream);
     GemmParams P{};
     P.w = w.seg[0];

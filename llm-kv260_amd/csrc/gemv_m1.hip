@@ -482,7 +482,7 @@ __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2
         b -= nblk;
     }
     if (j < 0) return;
-    GemvParams P;
+    GemvParams P{};
     derive_plain(P, B.e[j].w, B.e[j].x, B.e[j].y, B.e[j].rows, B.e[j].k);
     gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, lds);
 }

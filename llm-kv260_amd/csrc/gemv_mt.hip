@@ -35,6 +35,10 @@ constexpr int MT_MAX = 8;                        // tokens per launch
 constexpr int MT_THREADS = 512;
 constexpr size_t MT_LDS_BUDGET = 160 * 1024;
 
+#ifndef W4A8_MT_SPLIT
+#define W4A8_MT_SPLIT 1
+#endif
+
 struct MtParams {
     const uint8_t *w;
     const uint8_t *x;      // m rows of the engine layout, x_stride bytes apart
@@ -232,6 +236,133 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
     }
 }
 
+// Few tiles per CU (at most four: down at K = 8192): one tile per pair of
+// waves, each wave computing half the tokens, so that a SIMD holds two waves
+// whose LDS reads and dependent adds interleave, where one wave per SIMD
+// left them exposed. The pair loads the tile together (pieces 0-4 and 5-8),
+// stages it in the pair's slab, and after a workgroup barrier each wave
+// pulls its chunk. The pair's second buffer takes wave 1's terms, and the
+// slab, once both chunks are pulled, wave 0's. Every wave has exactly one
+// tile (the grid is sized so); past the last tile its loads read nothing and
+// it stores nothing. TG: tokens per wave, ceil(m / 2).
+template <int PASSES, int TG>
+__device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
+    const int nb = P.k >> 5;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nthreads = blockDim.x, waves = nthreads >> 6, pairs = waves >> 1;
+    const int slot = wave >> 1, half = wave & 1;
+    uint8_t *slab = lds + (size_t)slot * 2 * TILE_BYTES;
+    float *s_t = reinterpret_cast<float *>(slab + (size_t)half * TILE_BYTES);
+    uint32_t *s_x = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
+    const int tok_dwords = (int)(x_lds_bytes(nb) / 4);
+
+    const int C = P.C, rpw = P.rpw;
+    const int my_r = lane / C, my_c = lane - my_r * C;
+    const int colx = my_r < rpw ? my_c : 0;
+
+    // 1. The activation rows' loads, then this wave's pieces of the tile.
+    XRaw<X_ENGINE> xr[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int i = tid + p * nthreads;
+        const int t = i / nb, b = i - t * nb;
+        const bool live = t < P.m;
+        x_load<X_ENGINE>(P.x + (size_t)(live ? t : 0) * P.x_stride, P.k, b, live, xr[p]);
+    }
+    const int tile = block * pairs + slot;
+    u32x4 pc[5];
+    {
+        const size_t tile_bytes = (size_t)rpw * (size_t)C * CHUNK_BYTES;
+        const size_t total = (size_t)P.rows * (size_t)C * CHUNK_BYTES;
+        const size_t off0 = (size_t)__builtin_amdgcn_readfirstlane(tile) * tile_bytes;
+        const bool in = off0 < total;
+        const uint32_t n = in ? (uint32_t)(total - off0 < (size_t)TILE_BYTES ? total - off0 : (size_t)TILE_BYTES) : 0u;
+        const __amdgpu_buffer_rsrc_t tb = buffer_of(P.w + (in ? off0 : 0), n);
+#pragma unroll
+        for (int q = 0; q < 5; ++q) {
+            const int p = 5 * half + q;      // wave 1's fifth slot (p = 9) reads out of range
+            pc[q] = __builtin_amdgcn_raw_buffer_load_b128(tb, p < CHUNK_PIECES ? 1024 * p + 16 * lane : OUT_OF_RANGE,
+                                                          0, CACHE_NT);
+        }
+    }
+    // 2. Stage the activation; the tile into the slab; each wave's chunk.
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int i = tid + p * nthreads;
+        const int t = i / nb, b = i - t * nb;
+        if (t < P.m) x_stage<X_ENGINE>(xr[p], b, s_x + t * tok_dwords);
+    }
+    {
+        u32x4 *wslab = reinterpret_cast<u32x4 *>(slab);
+#pragma unroll
+        for (int q = 0; q < 5; ++q) {
+            const int p = 5 * half + q;
+            if (p < CHUNK_PIECES) wslab[64 * p + lane] = pc[q];
+        }
+    }
+    __syncthreads();
+    uint32_t w[CHUNK_DWORDS];
+    {
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(slab + CHUNK_BYTES * lane);
+#pragma unroll
+        for (int q = 0; q < CHUNK_PIECES; ++q) {
+            const u32x4 v = src[q];
+            w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+        }
+    }
+    __syncthreads();   // both chunks pulled: the slab takes wave 0's terms
+    uint32_t qs[8][4], dw[8], ns[8];
+#define W4A8_BLK(J)                           \
+    chunk_block<J>(w, dw[J], qs[J]);          \
+    ns[J] = nibble_sum(qs[J]);
+    W4A8_BLK(0) W4A8_BLK(1) W4A8_BLK(2) W4A8_BLK(3) W4A8_BLK(4) W4A8_BLK(5) W4A8_BLK(6) W4A8_BLK(7)
+#undef W4A8_BLK
+
+    // 3. This wave's tokens t0 .. t0 + TG - 1: terms, then their ordered sums
+    // in as few passes as the lanes allow (8 rpw lanes per token).
+    const int t0 = half * TG;
+    float term[TG][8];
+#pragma unroll
+    for (int u = 0; u < TG; ++u) {
+        const int t = t0 + u < P.m ? t0 + u : 0;          // past m: token 0 again, never stored
+        const uint32_t *col = s_x + t * tok_dwords + colx * XCOL_DWORDS;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(col + 8 * j);
+            const u32x4 a = src[0], c = src[1];
+            const uint32_t xn[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            const int32_t sumi = block_dot_with_sum(qs[j], ns[j], xn, (int32_t)col[XCOL_S + j]);
+            term[u][j] = block_term(sumi, dw[j], __uint_as_float(col[XCOL_D + j]));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < TG; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s_t[u * 576 + 9 * lane + j] = term[u][j];
+    wave_sync_lds();
+    const int acc_a = lane & 7;
+    const __amdgpu_buffer_rsrc_t y_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * P.rows * P.m, BUFFER_DWORD3);
+    const int per_tok = 8 * rpw, tok_pass = 64 / per_tok;
+    const int sum_u = lane / per_tok, sum_r = (lane - sum_u * per_tok) >> 3;
+    const int srow = tile * rpw + sum_r;
+    for (int u0 = 0; u0 < TG; u0 += tok_pass) {
+        const int u = u0 + sum_u;
+        const bool live = sum_u < tok_pass && u < TG;
+        const float yv = tree8_dpp(ordered_lane_sum(s_t + (live ? u : u0) * 576, sum_r, rpw, C, acc_a));
+        const bool store = live && acc_a == 0 && sum_r < rpw && srow < P.rows && t0 + u < P.m;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(yv), y_rsrc,
+                                              store ? 4 * ((t0 + u) * P.rows + srow) : OUT_OF_RANGE, 0, 0);
+    }
+}
+
+template <int PASSES, int TG>
+__global__ __launch_bounds__(MT_THREADS) void gemv_mt_split_kernel(MtParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    gemv_mt_split_body<PASSES, TG>(P, blockIdx.x, lds);
+}
+
 template <int PASSES, int TG, bool SHARED_SUMS>
 __global__ __launch_bounds__(MT_THREADS) void gemv_mt_kernel(MtParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -239,13 +370,20 @@ __global__ __launch_bounds__(MT_THREADS) void gemv_mt_kernel(MtParams P) {
 }
 
 template <int PASSES>
-hipError_t launch_mt_pass(const MtParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
+hipError_t launch_mt_pass(const MtParams &P, int grid, int threads, size_t lds, bool split, hipStream_t stream) {
     auto go = [&](const void *fn, auto kernel) {
         const hipError_t e = allow_dynamic_lds(fn, MT_LDS_BUDGET);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), lds, stream, P);
         return hipGetLastError();
     };
+    if (split) {
+        const int tg = (P.m + 1) / 2;
+        if (tg <= 1) return go(reinterpret_cast<const void *>(&gemv_mt_split_kernel<PASSES, 1>), gemv_mt_split_kernel<PASSES, 1>);
+        if (tg <= 2) return go(reinterpret_cast<const void *>(&gemv_mt_split_kernel<PASSES, 2>), gemv_mt_split_kernel<PASSES, 2>);
+        if (tg <= 3) return go(reinterpret_cast<const void *>(&gemv_mt_split_kernel<PASSES, 3>), gemv_mt_split_kernel<PASSES, 3>);
+        return go(reinterpret_cast<const void *>(&gemv_mt_split_kernel<PASSES, 4>), gemv_mt_split_kernel<PASSES, 4>);
+    }
     if (P.rpw <= 4) {
         if (P.m <= 2)
             return go(reinterpret_cast<const void *>(&gemv_mt_kernel<PASSES, 2, true>), gemv_mt_kernel<PASSES, 2, true>);
@@ -260,6 +398,27 @@ hipError_t launch_mt_pass(const MtParams &P, int grid, int threads, size_t lds, 
 bool gemv_mt_fits(int m, int rows, int k) {
     return m >= 2 && m <= MT_MAX && k >= 2048 && k <= 8192 && k % 256 == 0 &&
            (size_t)rows * (size_t)(k / QK * Q4_0_BYTES) < 0x7fff0000u && (size_t)m * rows * 4 < 0x7fff0000u;
+}
+
+int gemv_mt_max_m(int rows, int k) {
+#ifdef W4A8_MT_MAX_ALL
+    (void)rows; (void)k;
+    return W4A8_MT_MAX_ALL;
+#else
+    // Measured on MI355X against the MFMA kernels (rotated weights, us):
+    //  * m = 2 on every shape (q|k|v 4.3 against 4.9, o 4.2 against 4.8,
+    //    gate|up 6.7 against 8.4, down 5.5 against 9.5);
+    //  * m = 3, 4 from K = 4096 or 8,192 rows on (4096 x 4096 6.0-6.1
+    //    against 6.9, gate|up 8.0-8.1 against 8.3-8.4, 8192 x 2048 5.9
+    //    against 6.4, down 6.8-6.9 against 9.3-9.4); below that even;
+    //  * m = 5, 6 at K = 8192 where a tile's tokens are split over two waves
+    //    (down 8.1-8.2 against 9.3); at m = 7, 8 the two are even.
+    const int rpw = 64 / (k / 256 > 0 ? k / 256 : 1);
+    const int tiles = (rows + rpw - 1) / rpw;
+    if (k >= 8192 && W4A8_MT_SPLIT && tiles <= 4 * device_cu_count()) return 6;
+    if (rows >= 8192 || k >= 4096) return 4;
+    return 2;
+#endif
 }
 
 hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, int rows, int k, hipStream_t stream) {
@@ -284,7 +443,12 @@ hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, i
     //  * more (the LM head): four-wave workgroups striding over the matrix,
     //    two per CU.
     int waves, grid;
-    if (P.tiles <= 8 * cus) {
+    const bool split = W4A8_MT_SPLIT && P.tiles <= 4 * cus;
+    if (split) {
+        // One tile per pair of waves, four pairs per workgroup.
+        waves = 8;
+        grid = (P.tiles + 3) / 4;
+    } else if (P.tiles <= 8 * cus) {
         const int per_cu = (P.tiles + cus - 1) / cus;
         waves = per_cu < 4 ? 4 : per_cu;
         grid = (P.tiles + waves - 1) / waves;
@@ -297,10 +461,10 @@ hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, i
     const int passes = (m * nb + threads - 1) / threads;
     const size_t lds = (size_t)waves * TILE_BYTES + (size_t)m * x_lds_bytes(nb);
     if (lds > MT_LDS_BUDGET) return hipErrorInvalidValue;
-    if (passes <= 1) return launch_mt_pass<1>(P, grid, threads, lds, stream);
-    if (passes <= 2) return launch_mt_pass<2>(P, grid, threads, lds, stream);
-    if (passes <= 4) return launch_mt_pass<4>(P, grid, threads, lds, stream);
-    return launch_mt_pass<8>(P, grid, threads, lds, stream);
+    if (passes <= 1) return launch_mt_pass<1>(P, grid, threads, lds, split, stream);
+    if (passes <= 2) return launch_mt_pass<2>(P, grid, threads, lds, split, stream);
+    if (passes <= 4) return launch_mt_pass<4>(P, grid, threads, lds, split, stream);
+    return launch_mt_pass<8>(P, grid, threads, lds, split, stream);
 }
 
 }  // namespace w4a8

@@ -73,6 +73,8 @@ hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x_engine_rows, int m, 
 // The few-token GEMV (gemv_mt.hip): 2 <= m <= 8 engine-layout rows, k in
 // 2048..8192, the M = 1 kernel's weight stream with the arithmetic per token.
 bool gemv_mt_fits(int m, int rows, int k);
+// The largest m for which it is the faster kernel on this shape.
+int gemv_mt_max_m(int rows, int k);
 hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, int rows, int k, hipStream_t stream);
 // The row-split M > 1 kernel (gemm_rows.hip): m <= 64, k % 512 == 0.
 bool gemm_rows_fits(int rows, int k);

@@ -245,10 +245,13 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       (130, 8256, 1536),
                                       # the largest K, on both kernels
                                       (40, 64, 16384), (5, 8200, 16384),
-                                      # the few-token GEMV (m = 2, or m <= 4 on large matrices):
-                                      # ragged rows, one row, 48-chunk tiles (k = 6144), k = 8192
+                                      # the few-token GEMV (m = 2, or m <= 4 on large matrices, m <= 6
+                                      # where they have at most four tiles per CU and a tile's tokens
+                                      # are split over two waves): ragged rows, one row, 48-chunk tiles
+                                      # (k = 6144), k = 8192, odd m (a wave with a token past m)
                                       (2, 1, 4096), (2, 300, 6144), (3, 8200, 2048), (4, 8197, 2048),
-                                      (4, 2048, 8192), (3, 1000, 8192), (2, 5, 8192),
+                                      (4, 2048, 8192), (3, 1000, 8192), (2, 5, 8192), (5, 2048, 8192),
+                                      (6, 777, 8192), (5, 3, 8192),
                                       # 8-row items (K >= 8192, fewer 16-row groups than CUs): the
                                       # down shape, ragged rows, one item, several token groups
                                       (8, 2048, 8192), (5, 1003, 8192), (16, 8, 8192), (12, 2050, 8192),
