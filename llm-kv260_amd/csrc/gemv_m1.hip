@@ -247,12 +247,11 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
 // in the lane's register until the up tile's y is ready, and only
 // act[r] = silu_mul(gate, up) is stored, to y[0 .. rows / 2).
 template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false>
-__device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, uint8_t *lds) {
+__device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, int nthreads, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int nthreads = blockDim.x;
     const int waves = nthreads >> 6;
     uint8_t *slab = lds + (size_t)wave * TILE_BYTES;
     uint32_t *s_x = reinterpret_cast<uint32_t *>(lds + (size_t)waves * TILE_BYTES);
@@ -277,6 +276,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     // staging below waits for them only.
     XRaw<XF> xr;
     x_load<XF>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+
 
     uint32_t xv[8][8];
     float xd[8];
@@ -435,10 +435,28 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     if constexpr (ARGMAX) argmax_finish(P, best, nblocks, lds);
 }
 
+// The fields the first loads need (and the grid and workgroup sizes, which
+// otherwise come from the dispatch's hidden arguments) also come as leading
+// scalar arguments, which the build preloads into SGPRs: the first loads
+// then wait for no argument fetch. y is not among them: read from the
+// argument block with one scalar load at the start, as now, the decode chain
+// ran in 270 us per step; with y preloaded as well, so that the wave reads
+// nothing of the block, in 277 (the same as with nothing preloaded), and
+// delaying the weight loads by other means (a sleep, or a wait for the
+// activation's loads) did not recover it.
 template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false>
-__global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(GemvParams P) {
+__global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(const uint8_t *w0, const void *x, int rows, int k, int C,
+                                                              int rpw, int tiles, int nblocks, int nthreads,
+                                                              GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>(P, blockIdx.x, gridDim.x, lds);
+    P.seg[0] = w0;
+    P.x = x;
+    P.rows = rows;
+    P.k = k;
+    P.C = C;
+    P.rpw = rpw;
+    P.tiles = tiles;
+    gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>(P, blockIdx.x, nblocks, nthreads, lds);
 }
 
 __host__ __device__ inline void derive_plain(GemvParams &P, const uint8_t *w, const void *x, float *y, int rows, int k) {
@@ -484,7 +502,7 @@ __global__ __launch_bounds__(BATCH_THREADS) __attribute__((amdgpu_waves_per_eu(2
     if (j < 0) return;
     GemvParams P{};
     derive_plain(P, B.e[j].w, B.e[j].x, B.e[j].y, B.e[j].rows, B.e[j].k);
-    gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, lds);
+    gemv_m1_body<X_F32, true, ONE_PASS>(P, b, nblk, BATCH_THREADS, lds);
 }
 
 template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX, bool PAIR = false>
@@ -492,7 +510,8 @@ hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, h
     const hipError_t e =
         allow_dynamic_lds(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), LDS_BUDGET);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), dim3(grid), dim3(threads), lds, stream, P);
+    hipLaunchKernelGGL((gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), dim3(grid), dim3(threads), lds, stream,
+                       P.seg[0], P.x, P.rows, P.k, P.C, P.rpw, P.tiles, grid, threads, P);
     return hipGetLastError();
 }
 
