@@ -202,8 +202,8 @@ __device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lan
 }
 
 // LDS layout (dynamic): per-wave slabs [waves][9216] | the staged activation
-// (nb / 8 columns of XCOL_DWORDS) | for X_RMS the float64 squares of x (33 per
-// block) and the scale. `block` / `nblocks` are this workgroup's index and the
+// (nb / 8 columns of XCOL_DWORDS) | for X_RMS the float64 squares of x
+// (rms_sq_doubles(k), chain by chain) and the scale. `block` / `nblocks` are this workgroup's index and the
 // number of workgroups sharing the matrix.
 // ONE_PASS: a tile holds at most eight rows (K >= 2048), so one pass of the
 // ordered sums covers it and each lane stores at most one value per tile.
@@ -286,20 +286,21 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         float rms = 0.0f;
         if constexpr (XF == X_RMS) {
             // rmsnorm's scale needs the whole of x: its squares go to LDS as
-            // float64 after the staged x, wave 0 reduces them, and the scale
-            // comes back through LDS. Block b's 32 squares start at 33 b: the
-            // spare slot staggers the threads' 8-byte writes over the banks
-            // (at a stride of 32 they all hit the same two).
+            // float64 after the staged x (chain by chain, rms_sq_index), wave
+            // 0 reduces them, and the scale comes back through LDS. Block b's
+            // elements 32 b + 4 m + c are square 8 b + m of chain c.
             double *sq = reinterpret_cast<double *>(s_x + (nb / 8) * XCOL_DWORDS);
-            float *s_rms = reinterpret_cast<float *>(sq + P.k + P.k / 32);
+            float *s_rms = reinterpret_cast<float *>(sq + rms_sq_doubles(P.k));
+            const int cs = P.k / 4 + 2;
             auto squares = [&](const XRaw<XF> &r, int b) {
+                double *c0 = sq + 8 * b;
 #pragma unroll
                 for (int m = 0; m < 8; ++m) {
                     const double a = r.v[m].x, c = r.v[m].y, d = r.v[m].z, e = r.v[m].w;
-                    sq[33 * b + 4 * m] = a * a;
-                    sq[33 * b + 4 * m + 1] = c * c;
-                    sq[33 * b + 4 * m + 2] = d * d;
-                    sq[33 * b + 4 * m + 3] = e * e;
+                    c0[m] = a * a;
+                    c0[cs + m] = c * c;
+                    c0[2 * cs + m] = d * d;
+                    c0[3 * cs + m] = e * e;
                 }
             };
             if (tid < nb) squares(xr, tid);
@@ -310,7 +311,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             }
             __syncthreads();
             if (wave == 0) {
-                const float sc = rms_scale_wave<true>(sq, P.k, P.eps);
+                const float sc = rms_scale_wave(sq, P.k, P.eps);
                 if (lane == 0) *s_rms = sc;
             }
             __syncthreads();
@@ -603,7 +604,7 @@ hipError_t launch_gemv_m1(const MatrixRef &w, const void *x, XFormat xf, float *
     // Staged activation: int8 values, fp32 scale and int32 sum per block; for
     // X_RMS also the squares of x as float64 and the rmsnorm scale.
     if (xf == X_RMS && w.k > 8192) return hipErrorInvalidValue;
-    const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? (size_t)(w.k + w.k / 32) * 8 + 16 : 0);
+    const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? rms_sq_doubles(w.k) * 8 + 16 : 0);
     // Launch shape, from what bounds each size:
     //  * Small matrices (at most two tiles per CU): latency. One tile per
     //    wave, workgroups spread over every CU (each stages its own copy of
@@ -703,7 +704,7 @@ hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf
     const int half = P.tiles / 2;
     const int nb = k / QK;
     const int grid = half / waves;
-    const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? (size_t)(k + k / 32) * 8 + 16 : 0);
+    const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? rms_sq_doubles(k) * 8 + 16 : 0);
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
     if (xf == X_RMS) return launch_pass<X_RMS, true, true, false, true>(P, grid, 64 * waves, lds, stream);
     return launch_pass<X_F32, true, true, false, true>(P, grid, 64 * waves, lds, stream);

@@ -179,38 +179,62 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return sg * u;
 }
 
-// rmsnorm's scale (tp_llama.cpp:557-569) from sq[i] = (double)x[i]^2 in LDS
+// rmsnorm's scale (tp_llama.cpp:557-569) from the float64 squares of x
 // (exact: a float32 square fits a float64), n % 128 == 0: the sum of squares
-// accumulates in float64 in four lanes, element i in lane i % 4 in increasing
-// i (the reference's fused multiply-add of an exact square is this add); the
-// lanes meet as (l0 + l2) + (l1 + l3); then 1 / sqrtf((float)(ss / n) + eps).
-// Lanes 0..3 of the calling wave run the four chains of n / 4 dependent adds,
-// the next B squares read while the current B are added; the result is
-// returned in every lane of the wave. The squares are written by the whole
-// workgroup beforehand, so the chains carry the adds and nothing else.
-// PAD: square i is stored at i + i / 32 (a spare slot after every 32), the
-// layout of a workgroup whose threads each write one 32-element block.
-template <bool PAD = false>
-__device__ __forceinline__ float rms_scale_wave(const double *sq, int n, float eps) {
-    const int lane = threadIdx.x & 63;
-    auto at = [](int i) { return PAD ? i + (i >> 5) : i; };
+// accumulates in float64 in four chains, element i in chain i % 4 in
+// increasing i (the reference's fused multiply-add of an exact square is this
+// add); the chains meet as (c0 + c2) + (c1 + c3); then
+// 1 / sqrtf((float)(ss / n) + eps).
+//
+// Layout: chain c's squares lie contiguously, square i at rms_sq_index(i, n),
+// each chain n / 4 + 2 doubles after the last (a chain stride of 2 mod 32
+// doubles puts the four chains' 16-byte reads in distinct banks);
+// rms_sq_doubles(n) doubles in all, 16-byte aligned. The squares are written
+// by the whole workgroup beforehand, so the chains carry the adds and
+// nothing else: lane c of the calling wave runs chain c, two squares per
+// 16-byte read, the next four reads in flight while the current eight
+// squares are added. The result is returned in every lane of the wave.
+__host__ __device__ constexpr size_t rms_sq_doubles(int n) { return (size_t)n + 8; }
+__device__ __forceinline__ int rms_sq_index(int i, int n) { return (i & 3) * (n / 4 + 2) + (i >> 2); }
+
+template <int N>
+__device__ __forceinline__ double rms_chain(const double *sq, int n, int lane) {
+    constexpr int B = 4;                       // 16-byte reads per batch
+    const int len = N ? N : n;
+    const double2 *src = reinterpret_cast<const double2 *>(sq + lane * (len / 4 + 2));
+    const int pairs = len / 8;                 // a multiple of 2B: n % 128 == 0
     double acc = 0.0;
-    if (lane < 4) {
-        constexpr int B = 8;
-        double cur[B], nxt[B];
+    double2 a[B], b[B];
 #pragma unroll
-        for (int t = 0; t < B; ++t) cur[t] = sq[at(lane + 4 * t)];
-        for (int base = 0; base < n; base += 4 * B) {
-            // The last pass reads the first squares again (in range, unused).
-            const int next = base + 4 * B < n ? base + 4 * B : 0;
+    for (int t = 0; t < B; ++t) a[t] = src[t];
+    for (int p = 0; p < pairs; p += 2 * B) {
 #pragma unroll
-            for (int t = 0; t < B; ++t) nxt[t] = sq[at(next + lane + 4 * t)];
+        for (int t = 0; t < B; ++t) b[t] = src[p + B + t];
 #pragma unroll
-            for (int t = 0; t < B; ++t) acc = acc + cur[t];
+        for (int t = 0; t < B; ++t) {
+            acc = acc + a[t].x;
+            acc = acc + a[t].y;
+        }
+        // The last round reads the chain's first squares again (in range, unused).
+        const int q = p + 2 * B < pairs ? p + 2 * B : 0;
 #pragma unroll
-            for (int t = 0; t < B; ++t) cur[t] = nxt[t];
+        for (int t = 0; t < B; ++t) a[t] = src[q + t];
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            acc = acc + b[t].x;
+            acc = acc + b[t].y;
         }
     }
+    return acc;
+}
+
+__device__ __forceinline__ float rms_scale_wave(const double *sq, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    double acc = 0.0;
+    // The hidden size of the decode shapes with its trip count known (the
+    // compiler then unrolls the chain and issues its reads ahead of the
+    // adds); any other n in a loop.
+    if (lane < 4) acc = n == 2048 ? rms_chain<2048>(sq, n, lane) : rms_chain<0>(sq, n, lane);
     const double l1 = __shfl(acc, 1), l2 = __shfl(acc, 2), l3 = __shfl(acc, 3), l0 = __shfl(acc, 0);
     const double ss = (l0 + l2) + (l1 + l3);
     return 1.0f / sqrtf((float)(ss / (double)n) + eps);

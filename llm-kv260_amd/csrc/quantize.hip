@@ -130,13 +130,14 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_0_kernel(const float *__restri
     __shared__ float scale;
     const int row = blockIdx.x, nb = k >> 5;
     const float *xr = x + (size_t)row * k;
+    const int cs = k / 4 + 2;     // chain stride (rms_sq_index)
     for (int i = threadIdx.x; i < k / 4; i += blockDim.x) {
         const float4 v = reinterpret_cast<const float4 *>(xr)[i];
         const double a = v.x, b = v.y, c = v.z, d = v.w;
-        sq[4 * i] = a * a;
-        sq[4 * i + 1] = b * b;
-        sq[4 * i + 2] = c * c;
-        sq[4 * i + 3] = d * d;
+        sq[i] = a * a;
+        sq[cs + i] = b * b;
+        sq[2 * cs + i] = c * c;
+        sq[3 * cs + i] = d * d;
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -220,8 +221,8 @@ hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out
 hipError_t launch_rmsnorm_q8_0(const float *x, const float *w, float eps, int k, int m, uint8_t *out,
                                hipStream_t stream) {
     if (m <= 0) return hipSuccess;
-    const size_t lds = (size_t)k * 8;                       // float64 squares: 128 KB at k = 16384
-    const hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(&rmsnorm_q8_0_kernel), 128 * 1024);
+    const size_t lds = rms_sq_doubles(k) * 8;               // float64 squares: 128 KB at k = 16384
+    const hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(&rmsnorm_q8_0_kernel), 160 * 1024);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(rmsnorm_q8_0_kernel, dim3((unsigned)m), dim3(256), lds, stream, x, w, eps, k, out);
     return hipGetLastError();
