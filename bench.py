@@ -7,8 +7,11 @@ One step = one token's 65 W4A8 GEMVs (16 x q|k|v 3072x2048, o 2048x2048,
 gate|up 16384x2048, down 2048x8192, then the LM head 128256x2048), each
 preceded by the Q8_0 quantization of a float32 activation, in order: matrix
 j+1 starts after matrix j's output is complete, as in a decode. The step is
-issued by w4a8_chain_gemv (65 launches of the fused quantize + GEMV kernel),
-captured once into a HIP graph and replayed. Weights (695,107,584 bytes of
+a chain plan (w4a8_chain_plan_*: the 65 launches of the fused quantize + GEMV
+kernel as raw AQL dispatches on the library's own queue, no cache fences
+between them), launched for all timed steps at once and waited for; the same
+chain through w4a8_chain_gemv, captured into a HIP graph and replayed, is the
+chain_graph line. Weights (695,107,584 bytes of
 Q4_0) are resident in HBM; the chain alone is larger than the 256 MB Infinity
 Cache, so every step streams from HBM.
 
@@ -22,11 +25,13 @@ says "verified": true only when they all match. The GEMM sweep (configuration
 Prints one JSON line. Besides the chain (value), it reports:
   roofline     the chain's kernel (the fused quantize + GEMV, 65 launches per
                step): average algorithmic bytes per launch / average launch
-               duration, both over the timed region (HIP events on the launch
-               stream around the graph replays, launch boundaries included);
-               beside it, kernel_durations: the same bytes over the sum of the
-               65 kernels' average durations in the committed rocprofv3 trace
-               of `bench.py --chain-only`
+               duration, both over the timed region (the host clock around the
+               plan's launch and wait, dispatch boundaries included); beside
+               it, kernel_durations: the same bytes over the sum of the 65
+               kernels' average durations in the committed rocprofv3 trace of
+               `bench.py --chain-only`
+  chain_graph  the chain through w4a8_chain_gemv in a HIP graph (HIP events
+               on the launch stream around the replays), verified the same way
   chain_one_launch  the chain as one cooperative launch per step
                (W4A8_CHAIN_ONE_LAUNCH), verified the same way
   batch        the same 65 GEMVs per step in one w4a8_gemv_batch launch (no
@@ -514,7 +519,7 @@ def cpu_baseline(chain, mats, xs, budget_s=30.0):
     }
 
 
-def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic):
+def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph):
     """The fields every bench line carries: the metric, the chain and its roofline."""
     n = len(cf.decode_chain())
     chain_bytes = cf.chain_algorithmic_bytes()
@@ -548,29 +553,53 @@ def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd
                                "activation re-quantized to Q8_0 before every matrix, matrices in order",
                    "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
                    "algorithmic_bytes_per_step": chain_bytes},
-        "verified": (chain_check["ok"] and chain_check["weights_ok"] and
+        "verified": (chain_check["ok"] and chain_check["weights_ok"] and graph["verified"] and
                      (one_launch is None or one_launch["verified"])),
         "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("chain_traffic_bytes_per_launch"), "traffic_source": PMC_SUMMARY,
-                     "kernel": "gemv_m1_kernel<X_F32> (fused Q8_0 quantize + GEMV), the chain's 65 launches",
+                     "kernel": "w4a8_plan_gemv_f32 (gemv_m1_dev.h's fused Q8_0 quantize + GEMV), the chain "
+                               "plan's 65 dispatches",
                      "bytes_per_launch": round(chain_bytes / n), "us_per_launch": round(ms_per_step * 1e3 / n, 3),
-                     "timing": "HIP events on the launch stream around the timed graph replays: step time / 65, "
-                               "launch boundaries included",
+                     "timing": "host clock around the plan's timed launch and its wait, the device idle on both "
+                               "sides: step time / 65, dispatch boundaries included",
                      "kernel_durations": kernel},
         "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "gbps": round(chain_gbs, 1),
                   "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4), "launches_per_step": n,
+                  "issued_by": "w4a8_chain_plan_launch (raw AQL dispatches, no cache fences between steps)",
                   "verified": chain_check["ok"], "verification": chain_check,
                   "dependency": "matrix j+1 starts after matrix j's output is complete"},
+        "chain_graph": graph,
         "chain_one_launch": one_launch,
         "wall_s_timed": round(wall, 3),
     }
 
 
-def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd):
-    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, pmc_traffic() or {})
-    out["mode"] = "chain only" + ("" if one_launch is None else " (per-step chain, then the one-launch chain)")
+def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph):
+    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, pmc_traffic() or {}, graph)
+    out["mode"] = "chain only" + ("" if one_launch is None else " (plan, graph, then the one-launch chain)")
     return out
+
+
+def time_plan(torch, kv, L, ptr, n, steps, warmup, ys):
+    """ms per step of the chain plan: `warmup` passes, then exactly `steps`
+    passes in one launch, waited for; the device is idle (synchronized) on
+    both sides of the timed region and the outputs are poisoned before it."""
+    plan = ctypes.c_void_p()
+    kv.check("w4a8_chain_plan_create", L.w4a8_chain_plan_create(ptr, n, ctypes.byref(plan)))
+    try:
+        kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, max(warmup, 1)))
+        kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
+        poison(ys)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, steps))
+        kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 120000))
+        dt = time.perf_counter() - t0
+        torch.cuda.synchronize()
+    finally:
+        kv.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
+    return dt * 1e3 / steps, dt
 
 
 def main() -> int:
@@ -619,15 +648,27 @@ def main() -> int:
     ptr = ctypes.cast(steps, ctypes.c_void_p)
     chain_digests = [(r["name"], y, r["y"]) for y, r in zip(ys, recs)]
 
-    log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay)")
-    g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
-    ms_per_step, wall = time_replays(torch, stream, g_chain, args.steps, args.warmup, before=lambda: poison(ys))
+    log(f"timing {args.steps} steps after {args.warmup} warm-up steps (chain plan)")
+    ms_per_step, wall = time_plan(torch, kv, L, ptr, n, args.steps, args.warmup, ys)
     chain_check = verify(chain_digests)
     chain_check["weights_ok"] = weights_ok
     tok_s = 1e3 / ms_per_step
     chain_gbs = chain_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"chain: {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s, "
+    log(f"chain (plan): {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s, "
         f"outputs {'match' if chain_check['ok'] else 'DIFFER FROM'} the oracle's digests")
+
+    log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay of w4a8_chain_gemv)")
+    g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
+    ms_graph, _ = time_replays(torch, stream, g_chain, args.steps, args.warmup, before=lambda: poison(ys))
+    graph_check = verify(chain_digests)
+    graph = {"us_per_step": round(ms_graph * 1e3, 2), "tokens_per_s": round(1e3 / ms_graph, 1),
+             "gbps": round(chain_bytes / (ms_graph * 1e-3) / 1e9, 1),
+             "hbm_frac": round(chain_bytes / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "launches_per_step": n,
+             "kernel": "gemv_m1_kernel<X_F32>, 65 HIP launches per step from a graph",
+             "timing": "HIP events on the launch stream around the timed graph replays",
+             "verified": graph_check["ok"], "verification": graph_check}
+    log(f"chain (HIP graph): {graph['us_per_step']} us/step, {graph['tokens_per_s']} tokens/s, "
+        f"verified {graph['verified']}")
     del g_chain
 
     # The same chain as one cooperative launch per step (opt-in mode).
@@ -663,7 +704,7 @@ def main() -> int:
                 f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token), verified {r['verified']}")
     kd = kernel_durations() or {}
     if args.chain_only:
-        out = chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd)
+        out = chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph)
         print(json.dumps(out), flush=True)
         return 0 if out["verified"] else 1
 
@@ -714,13 +755,13 @@ def main() -> int:
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
         cpu = cpu_baseline(chain, mats, xs)
-    verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and
+    verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and graph["verified"] and
                 (one_launch is None or one_launch["verified"]) and
                 all(r["verified"] for r in gemm) and prefill[0]["verified"] is True)
 
-    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic)
+    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph)
     out["verified"] = verified
-    out["verification"] = {"chain": chain_check, "batch": batch_check,
+    out["verification"] = {"chain": chain_check, "chain_graph": graph_check, "batch": batch_check,
                            "one_launch": one_launch["verified"] if one_launch else None,
                            "gemm": {f"{r['name']} M={r['m']}": r["verified"] for r in gemm},
                            "prefill24": prefill[0]["verification"],

@@ -41,6 +41,9 @@ enum w4a8_status {
     W4A8_ERR_ALIGN = -3,   /* a pointer is not aligned as required */
     W4A8_ERR_HIP = -4,     /* the HIP runtime reported an error (w4a8_last_hip_error) */
     W4A8_ERR_NODEV = -5,   /* no usable gfx950 device */
+    /* -6: W4A8_ERR_FORMAT (w4a8_gguf.h) */
+    W4A8_ERR_TIMEOUT = -7, /* a bounded wait ran out (w4a8_chain_plan_wait) */
+    W4A8_ERR_HSA = -8,     /* the HSA runtime refused a queue, code object or signal */
 };
 
 /* "llm-kv260/w4a8-q4_0-v2": the contract these kernels are held to
@@ -228,6 +231,35 @@ int w4a8_chain_set_mode(int mode);
  * whenever every launch completed. A limit <= 0 restores the default. */
 int w4a8_chain_set_spin_limit(int polls);
 int w4a8_chain_timeouts(void);
+
+/* The same chain as a plan: made once, then launched any number of times.
+ * Each launch runs `passes` passes over the n steps, step j + 1 of a pass
+ * after step j, pass after pass, with the kernel of the per-step chain (every
+ * y byte-identical to w4a8_chain_gemv's). The steps are dispatched as raw
+ * AQL packets on a queue of the library's own (one per device), with no
+ * cache fences between consecutive steps: an output that a step of the plan
+ * reads is written through to the device's coherence point and read from
+ * there, found by comparing the steps' ranges when the plan is made. That
+ * saves the two fences the HIP runtime puts around every kernel of a stream
+ * or graph. It is not ordered with HIP streams, as the reference's engine is
+ * driven by start and wait calls (board/kv260gemv/gemv2_dev.h:40-44):
+ *   - create: steps as for w4a8_chain_gemv, every k in 2048..W4A8_MAX_K; the
+ *     plan belongs to the current device and keeps the pointers (the
+ *     buffers must stay allocated, their contents may change between
+ *     launches); 1 <= n <= W4A8_CHAIN_MAX_STEPS;
+ *   - launch: returns once the packets are written; whatever writes the
+ *     plan's x or weights must be complete before it (e.g.
+ *     hipStreamSynchronize); 1 <= passes <= 1 << 20;
+ *   - wait: until every launch of the plan so far is done, at most
+ *     timeout_ms (W4A8_ERR_TIMEOUT); after W4A8_OK the outputs are visible
+ *     to the host and to any later HIP work;
+ *   - destroy: waits (at most 10 s) and frees the plan.
+ * Launches of plans on one device go to that device's queue in call order. */
+typedef struct w4a8_chain_plan w4a8_chain_plan;
+int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan);
+int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes);
+int w4a8_chain_plan_wait(w4a8_chain_plan *plan, int timeout_ms);
+int w4a8_chain_plan_destroy(w4a8_chain_plan *plan);
 
 /* The same n GEMVs with no order between them, in one launch: every matrix
  * streams at once, so small matrices no longer pay a launch and a latency

@@ -56,6 +56,8 @@ const char *w4a8_strerror(int status) {
         case W4A8_ERR_HIP: return "HIP runtime error";
         case W4A8_ERR_NODEV: return "no usable gfx950 device";
         case W4A8_ERR_FORMAT: return "not a GGUF file, or a malformed one";
+        case W4A8_ERR_TIMEOUT: return "a bounded wait ran out";
+        case W4A8_ERR_HSA: return "HSA runtime error (queue, code object or signal)";
         default: return "unknown status";
     }
 }
@@ -220,6 +222,35 @@ int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream) {
     for (int i = 0; i < n; ++i)
         if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
     return hip_status(launch_chain(steps, n, (hipStream_t)stream));
+}
+
+int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan) {
+    if (!steps || !plan) return W4A8_ERR_NULL;
+    *plan = nullptr;
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
+    for (int i = 0; i < n; ++i) {
+        if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
+        if (steps[i].k < 2048) return W4A8_ERR_SHAPE;
+    }
+    hipError_t he = hipSuccess;
+    const int s = chain_plan_create(steps, n, plan, he);
+    return s == W4A8_ERR_HIP ? hip_status(he) : s;
+}
+
+int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes) {
+    if (!plan) return W4A8_ERR_NULL;
+    if (passes < 1 || passes > (1 << 20)) return W4A8_ERR_SHAPE;
+    return chain_plan_launch(plan, passes);
+}
+
+int w4a8_chain_plan_wait(w4a8_chain_plan *plan, int timeout_ms) {
+    if (!plan) return W4A8_ERR_NULL;
+    return chain_plan_wait(plan, timeout_ms < 0 ? 0 : timeout_ms);
+}
+
+int w4a8_chain_plan_destroy(w4a8_chain_plan *plan) {
+    if (!plan) return W4A8_OK;
+    return chain_plan_destroy(plan);
 }
 
 int w4a8_chain_set_mode(int mode) {

@@ -68,7 +68,6 @@ constexpr int CHAIN_MIN_K = 2048;              // one pass of ordered sums per t
 constexpr int CHAIN_MAX_K = 8192;
 constexpr size_t RING_BYTES = (size_t)RING * TILE_BYTES;
 constexpr size_t CHAIN_LDS = RING_BYTES + x_lds_bytes(CHAIN_MAX_K / QK);
-constexpr uint32_t SC1 = 16;                   // device-scope coherent access (sc1)
 constexpr int DEFAULT_SPIN_LIMIT = 1 << 22;    // polls (~0.5 us each) before a wait gives up
 
 // One step as the kernel takes it (32 bytes), its tile geometry worked out on

@@ -1,0 +1,284 @@
+// The decode step's GEMV chain as a plan: the per-step chain's kernel
+// (gemv_m1_dev.h, fp32 x quantized in its staging), dispatched as raw AQL
+// packets on an HSA queue of the library's own (one per device) instead of
+// through HIP launches.
+//
+// Why: between two kernels of a HIP stream or graph the packet processor
+// runs a release fence (every XCD's L2 written back) and an acquire fence
+// (every L2 and the scalar caches invalidated). The chain's kernels are
+// small and dependent, so those fences sit on the critical path 65 times
+// per token. A plan's packets carry no fences between steps (acquire at
+// system scope on a launch's first packet, release at system scope on its
+// last) and keep only the barrier bit, which orders step j + 1 after step j.
+// What the fences did for the chain's own data is done per step instead:
+// an output that a later step reads is written through to the device's
+// coherence point and waited for before its waves end, and that step reads
+// it from there (the kernels' _yc / _xc variants); everything else goes
+// through the caches as before. The kernel arguments sit in device memory,
+// written once when the plan is made.
+//
+// This mirrors how the reference drives its engine: the host starts the
+// work and later waits for it (board/kv260gemv/gemv2_dev.h:40-44,
+// board/tp/tp_llama.cpp:318-323), not through a stream.
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
+
+#include <chrono>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "gemv_m1_dev.h"
+
+extern "C" const char w4a8_chain_plan_co_begin[];
+extern "C" const char w4a8_chain_plan_co_end[];
+
+struct w4a8_chain_plan {
+    int device = 0;
+    int n = 0;
+    std::vector<int> kind;                 // kernel variant per step
+    std::vector<uint32_t> grid, threads, group;
+    char *kargs = nullptr;                 // device memory, ARG_STRIDE bytes per step
+    hsa_signal_t done{};                   // launches in flight
+};
+
+namespace w4a8 {
+
+namespace {
+
+// The kernels' argument block (their kernarg segment is exactly this).
+struct PlanArgs {
+    const uint8_t *w0;
+    const void *x;
+    int rows, k, C, rpw, tiles, nblocks, nthreads, pad;
+    GemvParams P;
+};
+static_assert(sizeof(PlanArgs) == 176, "argument block of the plan's kernels");
+constexpr size_t ARG_STRIDE = 256;
+constexpr uint32_t QUEUE_PACKETS = 16384;
+constexpr const char *KERNEL_NAMES[4] = {"w4a8_plan_gemv_f32.kd", "w4a8_plan_gemv_f32_xc.kd", "w4a8_plan_gemv_f32_yc.kd",
+                                         "w4a8_plan_gemv_f32_xyc.kd"};
+constexpr double QUEUE_SPACE_WAIT_S = 10.0;    // bound on waiting for free packet slots
+
+struct DeviceRuntime {
+    std::mutex m;                  // one producer on the queue at a time
+    bool tried = false;
+    int status = W4A8_OK;
+    hsa_agent_t agent{};
+    hsa_queue_t *queue = nullptr;
+    hsa_executable_t exe{};
+    uint64_t kobj[4]{};
+    uint32_t group[4]{}, priv[4]{};
+};
+constexpr int MAX_DEVICES = 16;
+DeviceRuntime g_rt[MAX_DEVICES];
+
+struct AgentMatch {
+    uint32_t domain, bdf;
+    hsa_agent_t agent;
+    bool found;
+};
+
+hsa_status_t match_agent(hsa_agent_t a, void *data) {
+    auto *m = static_cast<AgentMatch *>(data);
+    hsa_device_type_t t;
+    if (hsa_agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS || t != HSA_DEVICE_TYPE_GPU)
+        return HSA_STATUS_SUCCESS;
+    uint32_t bdf = 0, domain = 0;
+    if (hsa_agent_get_info(a, (hsa_agent_info_t)HSA_AMD_AGENT_INFO_BDFID, &bdf) != HSA_STATUS_SUCCESS ||
+        hsa_agent_get_info(a, (hsa_agent_info_t)HSA_AMD_AGENT_INFO_DOMAIN, &domain) != HSA_STATUS_SUCCESS)
+        return HSA_STATUS_SUCCESS;
+    if (bdf == m->bdf && domain == m->domain) {
+        m->agent = a;
+        m->found = true;
+        return HSA_STATUS_INFO_BREAK;
+    }
+    return HSA_STATUS_SUCCESS;
+}
+
+// The HSA agent of HIP device `dev`, the plan kernels loaded for it and its
+// queue; made once per device.
+int runtime_of(int dev, DeviceRuntime *&out) {
+    if (dev < 0 || dev >= MAX_DEVICES) return W4A8_ERR_NODEV;
+    DeviceRuntime &rt = g_rt[dev];
+    std::lock_guard<std::mutex> lk(rt.m);
+    out = &rt;
+    if (rt.tried) return rt.status;
+    rt.tried = true;
+    rt.status = W4A8_ERR_HSA;
+    int bus = 0, devid = 0, domain = 0;
+    if (hipDeviceGetAttribute(&bus, hipDeviceAttributePciBusId, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&devid, hipDeviceAttributePciDeviceId, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&domain, hipDeviceAttributePciDomainID, dev) != hipSuccess)
+        return rt.status = W4A8_ERR_NODEV;
+    if (hsa_init() != HSA_STATUS_SUCCESS) return rt.status;
+    AgentMatch m{(uint32_t)domain, ((uint32_t)bus << 8) | ((uint32_t)devid << 3), {}, false};
+    const hsa_status_t it = hsa_iterate_agents(match_agent, &m);
+    if ((it != HSA_STATUS_SUCCESS && it != HSA_STATUS_INFO_BREAK) || !m.found) return rt.status = W4A8_ERR_NODEV;
+    rt.agent = m.agent;
+    hsa_code_object_reader_t rd;
+    const size_t co_bytes = (size_t)(w4a8_chain_plan_co_end - w4a8_chain_plan_co_begin);
+    if (hsa_code_object_reader_create_from_memory(w4a8_chain_plan_co_begin, co_bytes, &rd) != HSA_STATUS_SUCCESS)
+        return rt.status;
+    if (hsa_executable_create_alt(HSA_PROFILE_FULL, HSA_DEFAULT_FLOAT_ROUNDING_MODE_DEFAULT, nullptr, &rt.exe) !=
+            HSA_STATUS_SUCCESS ||
+        hsa_executable_load_agent_code_object(rt.exe, rt.agent, rd, nullptr, nullptr) != HSA_STATUS_SUCCESS ||
+        hsa_executable_freeze(rt.exe, nullptr) != HSA_STATUS_SUCCESS)
+        return rt.status;
+    for (int v = 0; v < 4; ++v) {
+        hsa_executable_symbol_t sym;
+        if (hsa_executable_get_symbol_by_name(rt.exe, KERNEL_NAMES[v], &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
+            hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &rt.kobj[v]) !=
+                HSA_STATUS_SUCCESS ||
+            hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE, &rt.group[v]) !=
+                HSA_STATUS_SUCCESS ||
+            hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE, &rt.priv[v]) !=
+                HSA_STATUS_SUCCESS)
+            return rt.status;
+    }
+    if (hsa_queue_create(rt.agent, QUEUE_PACKETS, HSA_QUEUE_TYPE_SINGLE, nullptr, nullptr, UINT32_MAX, UINT32_MAX,
+                         &rt.queue) != HSA_STATUS_SUCCESS)
+        return rt.status;
+    return rt.status = W4A8_OK;
+}
+
+bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + nb && y < x + na;
+}
+
+}  // namespace
+
+int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out, hipError_t &he) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return W4A8_ERR_NODEV;
+    DeviceRuntime *rt = nullptr;
+    if (const int s = runtime_of(dev, rt)) return s;
+    auto *p = new w4a8_chain_plan();
+    p->device = dev;
+    p->n = n;
+    p->kind.assign(n, 0);
+    // Which outputs another step reads, in this pass or the next.
+    for (int j = 0; j < n; ++j)
+        for (int i = 0; i < n; ++i)
+            if (overlaps(steps[j].x, 4 * (size_t)steps[j].k, steps[i].y, 4 * (size_t)steps[i].rows)) {
+                p->kind[j] |= COH_X;
+                p->kind[i] |= COH_Y;
+            }
+    const int cus = device_cu_count();
+    std::vector<PlanArgs> args(n);
+    for (int j = 0; j < n; ++j) {
+        const w4a8_chain_step &s = steps[j];
+        const int C = s.k / 256, rpw = 64 / C, tiles = (s.rows + rpw - 1) / rpw;
+        const M1Shape sh = gemv_m1_shape(tiles, s.k, X_F32, false, cus);
+        PlanArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.w0 = static_cast<const uint8_t *>(s.w);
+        a.x = s.x;
+        a.rows = s.rows;
+        a.k = s.k;
+        a.C = C;
+        a.rpw = rpw;
+        a.tiles = tiles;
+        a.nblocks = sh.grid;
+        a.nthreads = sh.threads;
+        for (int g = 0; g < 4; ++g) a.P.seg[g] = a.w0;
+        a.P.x = s.x;
+        a.P.y = s.y;
+        a.P.seg_rows = s.rows;
+        a.P.nseg = 1;
+        a.P.k = s.k;
+        a.P.rows = s.rows;
+        a.P.C = C;
+        a.P.rpw = rpw;
+        a.P.tiles = tiles;
+        args[j] = a;
+        p->grid.push_back((uint32_t)sh.grid);
+        p->threads.push_back((uint32_t)sh.threads);
+        p->group.push_back(rt->group[p->kind[j]] + (uint32_t)sh.lds);
+    }
+    std::vector<char> host((size_t)n * ARG_STRIDE, 0);
+    for (int j = 0; j < n; ++j) std::memcpy(host.data() + (size_t)j * ARG_STRIDE, &args[j], sizeof(PlanArgs));
+    hipError_t e = hipMalloc(&p->kargs, host.size());
+    if (e == hipSuccess) e = hipMemcpy(p->kargs, host.data(), host.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (p->kargs) (void)hipFree(p->kargs);
+        delete p;
+        he = e;
+        return W4A8_ERR_HIP;
+    }
+    if (hsa_signal_create(0, 0, nullptr, &p->done) != HSA_STATUS_SUCCESS) {
+        (void)hipFree(p->kargs);
+        delete p;
+        return W4A8_ERR_HSA;
+    }
+    *out = p;
+    return W4A8_OK;
+}
+
+int chain_plan_launch(w4a8_chain_plan *p, int passes) {
+    DeviceRuntime *rt = nullptr;
+    if (const int s = runtime_of(p->device, rt)) return s;
+    std::lock_guard<std::mutex> lk(rt->m);
+    hsa_queue_t *q = rt->queue;
+    const long total = (long)passes * p->n;
+    hsa_signal_add_relaxed(p->done, 1);
+    uint64_t idx = 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (long i = 0; i < total; ++i) {
+        const int j = (int)(i % p->n);
+        idx = hsa_queue_add_write_index_relaxed(q, 1);
+        // A full queue: ring for what is written, then wait (bounded) for room.
+        while (idx - hsa_queue_load_read_index_scacquire(q) >= q->size) {
+            hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx - 1);
+            if (std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > QUEUE_SPACE_WAIT_S)
+                return W4A8_ERR_TIMEOUT;   // the slots taken stay unwritten: the queue is unusable after this
+        }
+        auto *pk = reinterpret_cast<hsa_kernel_dispatch_packet_t *>(q->base_address) + (idx & (q->size - 1));
+        std::memset(reinterpret_cast<char *>(pk) + 4, 0, sizeof(*pk) - 4);
+        const int v = p->kind[j];
+        pk->workgroup_size_x = (uint16_t)p->threads[j];
+        pk->workgroup_size_y = 1;
+        pk->workgroup_size_z = 1;
+        pk->grid_size_x = p->grid[j] * p->threads[j];
+        pk->grid_size_y = 1;
+        pk->grid_size_z = 1;
+        pk->private_segment_size = rt->priv[v];
+        pk->group_segment_size = p->group[j];
+        pk->kernel_object = rt->kobj[v];
+        pk->kernarg_address = p->kargs + (size_t)j * ARG_STRIDE;
+        const bool first = i == 0, last = i == total - 1;
+        if (last) pk->completion_signal = p->done;
+        const uint16_t header =
+            (uint16_t)((HSA_PACKET_TYPE_KERNEL_DISPATCH << HSA_PACKET_HEADER_TYPE) | (1 << HSA_PACKET_HEADER_BARRIER) |
+                       ((first ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_NONE) << HSA_PACKET_HEADER_SCACQUIRE_FENCE_SCOPE) |
+                       ((last ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_NONE) << HSA_PACKET_HEADER_SCRELEASE_FENCE_SCOPE));
+        const uint32_t setup = 1u << HSA_KERNEL_DISPATCH_PACKET_SETUP_DIMENSIONS;
+        __atomic_store_n(&pk->full_header, (uint32_t)header | (setup << 16), __ATOMIC_RELEASE);
+        // Ring once per pass, so the device starts while later passes are written.
+        if (j == p->n - 1) hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
+    }
+    return W4A8_OK;
+}
+
+int chain_plan_wait(w4a8_chain_plan *p, int timeout_ms) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (;;) {
+        const hsa_signal_value_t v =
+            hsa_signal_wait_scacquire(p->done, HSA_SIGNAL_CONDITION_LT, 1, 1000000, HSA_WAIT_STATE_ACTIVE);
+        if (v < 1) return W4A8_OK;
+        if (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() > timeout_ms)
+            return W4A8_ERR_TIMEOUT;
+    }
+}
+
+int chain_plan_destroy(w4a8_chain_plan *p) {
+    const int s = chain_plan_wait(p, 10000);
+    if (s != W4A8_OK) return s;   // work in flight: the plan stays valid
+    hsa_signal_destroy(p->done);
+    (void)hipFree(p->kargs);
+    delete p;
+    return W4A8_OK;
+}
+
+}  // namespace w4a8

@@ -19,6 +19,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int OUT_OF_RANGE = 0x7ffffff0;
 constexpr uint32_t BUFFER_DWORD3 = 0x00020000;   // raw dword access on gfx9-family parts
 constexpr int CACHE_NT = 2;                       // non-temporal (streamed once)
+constexpr int SC1 = 16;                           // device-scope coherent access (sc1)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, BUFFER_DWORD3);
@@ -51,20 +52,23 @@ struct XRaw<X_SILU> {
     float4 u[8];   // up
 };
 
+template <int AUX = 0>
 __device__ __forceinline__ void load_f32_block(__amdgpu_buffer_rsrc_t rb, int off, float4 v[8]) {
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rb, off == OUT_OF_RANGE ? OUT_OF_RANGE : off + 16 * m, 0, 0);
+        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rb, off == OUT_OF_RANGE ? OUT_OF_RANGE : off + 16 * m, 0, AUX);
         v[m] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
     }
 }
 
-// Block b of the activation; a lane with live == false reads nothing.
-template <int XF>
+// Block b of the activation; a lane with live == false reads nothing. AUX:
+// the cache policy of the fp32 x's loads (SC1: from the device's coherence
+// point, for an x that an earlier dispatch with no fence after it wrote).
+template <int XF, int AUX = 0>
 __device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, XRaw<XF> &r,
                                        const float *norm_w = nullptr) {
     if constexpr (XF == X_RMS) {
-        load_f32_block(buffer_of(x, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.v);
+        load_f32_block<AUX>(buffer_of(x, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.v);
         load_f32_block(buffer_of(norm_w, (uint32_t)(4 * k)), live ? 128 * b : OUT_OF_RANGE, r.w);
     } else if constexpr (XF == X_SILU) {
         const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(8 * k));
@@ -86,7 +90,7 @@ __device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, X
         const int off = live ? 128 * b : OUT_OF_RANGE;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xb, off + 16 * m, 0, 0);
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xb, off + 16 * m, 0, AUX);
             r.v[m] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
         }
     }
@@ -201,8 +205,9 @@ __device__ __forceinline__ void wave_sync_lds() {
 // issues the instruction, so the number of memory operations a wave has in
 // flight never depends on data, and the waits for the prefetched tiles stay
 // exact.
+template <int AUX = 0>
 __device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t y, int byte_off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y, byte_off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y, byte_off, 0, AUX);
 }
 
 

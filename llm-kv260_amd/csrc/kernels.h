@@ -49,6 +49,14 @@ int device_cu_count();            // of the current device (cached per device)
 // Thread-safe.
 hipError_t allow_dynamic_lds(const void *fn, size_t budget);
 
+// The M = 1 GEMV's launch shape for a matrix of `tiles` wave tiles (64 / (k /
+// 256) rows each): workgroups, threads per workgroup, dynamic LDS bytes.
+struct M1Shape {
+    int grid, threads;
+    size_t lds;
+};
+M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool argmax, int cus);
+
 // argmax != null: also *argmax = the first row of the largest y, reduced in the
 // same launch through `workspace` (argmax_workspace_bytes(), zero between
 // calls); x must then be X_F32 or X_RMS.
@@ -92,6 +100,7 @@ hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out
 }  // namespace w4a8
 
 struct w4a8_chain_step;   // include/w4a8.h
+struct w4a8_chain_plan;   // chain_plan.hip
 
 namespace w4a8 {
 
@@ -101,6 +110,12 @@ namespace w4a8 {
 hipError_t launch_chain(const w4a8_chain_step *steps, int n, hipStream_t stream);
 bool chain_one_launch_fits(const w4a8_chain_step *steps, int n);
 hipError_t launch_chain_one(const w4a8_chain_step *steps, int n, hipStream_t stream);
+// The chain plan (chain_plan.hip): statuses as the C ABI's; a HIP error of
+// create comes back in `he` with W4A8_ERR_HIP.
+int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out, hipError_t &he);
+int chain_plan_launch(w4a8_chain_plan *p, int passes);
+int chain_plan_wait(w4a8_chain_plan *p, int timeout_ms);
+int chain_plan_destroy(w4a8_chain_plan *p);
 // The one-launch chain's bounded waits: polls before a wait gives up
 // (<= 0 restores the default), and the count of launches on the current
 // device that gave up since the last call (read and cleared; synchronous).

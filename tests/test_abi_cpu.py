@@ -91,6 +91,18 @@ def test_argument_checks_come_before_the_device():
     assert L.w4a8_chain_gemv(None, 1, None) == -1
     quarters = (ctypes.c_void_p * 4)(fake, fake, None, fake)
     assert L.w4a8_gemv_quarters(quarters, fake, fake, 16, 2048, None) == -1
+    plan = ctypes.c_void_p()
+    assert L.w4a8_chain_plan_create(None, 1, ctypes.byref(plan)) == -1
+    steps = (ctypes.c_void_p * 3)(fake, fake, fake)
+    raw = (ctypes.c_int * 2)(16, 1024)                 # one step, k = 1024 < 2048
+    buf = ctypes.create_string_buffer(bytes(steps) + bytes(raw))
+    assert L.w4a8_chain_plan_create(buf, 1, ctypes.byref(plan)) == -2
+    assert L.w4a8_chain_plan_create(buf, 0, ctypes.byref(plan)) == -2
+    assert L.w4a8_chain_plan_create(buf, 1, None) == -1
+    assert L.w4a8_chain_plan_launch(None, 1) == -1
+    assert L.w4a8_chain_plan_wait(None, 0) == -1
+    assert L.w4a8_chain_plan_destroy(None) == 0
+    assert kv260gemv.strerror(-7).startswith("a bounded wait")
 
 
 class Udmabuf(ctypes.Structure):

@@ -1,0 +1,187 @@
+"""The decode chain as a plan (w4a8_chain_plan_*: raw AQL dispatches on the
+library's own queue, no cache fences between steps): each step byte for byte
+against the oracle and against w4a8_chain_gemv, over several passes and
+launches; a step-to-step data dependency inside a pass and one that runs from
+the last step of a pass into the first step of the next (the coherent-read
+and write-through variants); several launches before one wait; plans made
+and destroyed in turn.
+
+Every output buffer is poisoned with 0xAA first.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import c_oracle as C
+import q4_0_oracle as O
+from gpu_helpers import assert_bytes_equal, dev, host, poisoned_f32
+
+pytestmark = pytest.mark.gpu
+
+
+class Step(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("rows", ctypes.c_int), ("k", ctypes.c_int)]
+
+
+def _steps(mats, xs, ys, shapes):
+    return (Step * len(shapes))(*[Step(mats[i].data_ptr(), xs[i].data_ptr(), ys[i].data_ptr(), r, k)
+                                  for i, (r, k) in enumerate(shapes)])
+
+
+class Plan:
+    def __init__(self, gpu, steps, n):
+        import torch
+        torch.cuda.synchronize()       # the plan's queue is not ordered with HIP streams
+        self.L, self.gpu = gpu.lib(), gpu
+        self.p = ctypes.c_void_p()
+        gpu.check("w4a8_chain_plan_create", self.L.w4a8_chain_plan_create(ctypes.cast(steps, ctypes.c_void_p), n,
+                                                                          ctypes.byref(self.p)))
+
+    def run(self, passes=1):
+        self.gpu.check("w4a8_chain_plan_launch", self.L.w4a8_chain_plan_launch(self.p, passes))
+        self.gpu.check("w4a8_chain_plan_wait", self.L.w4a8_chain_plan_wait(self.p, 30000))
+
+    def close(self):
+        self.gpu.check("w4a8_chain_plan_destroy", self.L.w4a8_chain_plan_destroy(self.p))
+
+
+def _independent(shapes, seed0):
+    mats, xs, ys, wants = [], [], [], []
+    for i, (rows, k) in enumerate(shapes):
+        blocks = C.quantize_q4_0(O.normal_f32((rows, k), seed0 + i, 0.02))
+        x = O.normal_f32((1, k), seed0 + 500 + i)[0]
+        xq, xd = C.quantize_q8_0(x)
+        mats.append(dev(blocks))
+        xs.append(dev(x))
+        ys.append(poisoned_f32(rows))
+        wants.append(C.gemv_q4_0(blocks, k, xq, xd))
+    return mats, xs, ys, wants
+
+
+SHAPES = {
+    # the layer shapes and a ragged LM-head-like tail (the large launch shape)
+    "llama_layer": [(3072, 2048), (2048, 2048), (16384, 2048), (2048, 8192), (20000, 2048)],
+    # one row, ragged rows, a tile of fewer than 64 chunks (k = 6144), k = 16384
+    "ragged": [(1, 2048), (5, 4096), (300, 6144), (257, 8192), (9, 2048), (4097, 4096), (33, 16384)],
+    "single": [(64, 2048)],
+}
+
+
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_plan_matches_oracle_and_chain(gpu, name):
+    import torch
+    shapes = SHAPES[name]
+    mats, xs, ys, wants = _independent(shapes, 1500)
+    steps = _steps(mats, xs, ys, shapes)
+    plan = Plan(gpu, steps, len(shapes))
+    plan.run(1)
+    for i, (y, want) in enumerate(zip(ys, wants)):
+        assert_bytes_equal(host(y), want, f"{name} step {i} {shapes[i]}")
+    for passes in (3, 1):
+        for y in ys:
+            y.fill_(float("nan"))
+        plan.run(passes)
+        for i, (y, want) in enumerate(zip(ys, wants)):
+            assert_bytes_equal(host(y), want, f"{name} {passes} passes, step {i}")
+    plan.close()
+    for y in ys:
+        y.fill_(float("nan"))
+    L = gpu.lib()
+    gpu.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ctypes.cast(steps, ctypes.c_void_p), len(shapes),
+                                                   torch.cuda.current_stream().cuda_stream))
+    for i, (y, want) in enumerate(zip(ys, wants)):
+        assert_bytes_equal(host(y), want, f"{name} step {i}: w4a8_chain_gemv")
+
+
+def _dependent_oracle(blocks, shapes, x0, passes):
+    """The chain y_j = W_j q8(y_{j-1}) run `passes` times on the CPU; with
+    `cyclic`, pass p + 1 starts from pass p's last output."""
+    x, outs = x0, None
+    for _ in range(passes):
+        outs = []
+        for b, (r, k) in zip(blocks, shapes):
+            xq, xd = C.quantize_q8_0(x)
+            x = C.gemv_q4_0(b, k, xq, xd)
+            outs.append(x)
+    return outs
+
+
+def test_plan_dependency_inside_a_pass(gpu):
+    """x of every step after the first IS the previous step's y."""
+    shapes = [(2048, 2048), (8192, 2048), (2048, 8192), (2048, 2048), (3072, 2048), (2048, 3072), (2048, 2048)]
+    blocks = [C.quantize_q4_0(O.normal_f32((r, k), 60 + i, 0.02)) for i, (r, k) in enumerate(shapes)]
+    x0 = O.normal_f32((1, shapes[0][1]), 59)[0]
+    wants = _dependent_oracle(blocks, shapes, x0, 1)
+    mats = [dev(b) for b in blocks]
+    xin = dev(x0)
+    ys = [poisoned_f32(r) for r, _ in shapes]
+    plan = Plan(gpu, _steps(mats, [xin] + ys[:-1], ys, shapes), len(shapes))
+    for passes in (1, 4, 2):
+        for y in ys:
+            y.fill_(float("nan"))
+        plan.run(passes)
+        for i, (y, want) in enumerate(zip(ys, wants)):
+            assert_bytes_equal(host(y), want, f"{passes} passes, step {i}")
+    plan.close()
+
+
+def test_plan_dependency_across_passes(gpu):
+    """The first step reads the last step's output: each pass continues from
+    the previous one, within a launch and across launches."""
+    shapes = [(8192, 2048), (2048, 8192), (3072, 2048), (2048, 3072)]
+    blocks = [C.quantize_q4_0(O.normal_f32((r, k), 80 + i, 0.02)) for i, (r, k) in enumerate(shapes)]
+    x0 = O.normal_f32((1, 2048), 79)[0]
+    mats = [dev(b) for b in blocks]
+    ys = [poisoned_f32(r) for r, _ in shapes]
+    ys[-1].copy_(dev(x0))                  # the first pass starts from x0
+    plan = Plan(gpu, _steps(mats, [ys[-1]] + ys[:-1], ys, shapes), len(shapes))
+    plan.run(3)
+    wants = _dependent_oracle(blocks, shapes, x0, 3)
+    for i, (y, want) in enumerate(zip(ys, wants)):
+        assert_bytes_equal(host(y), want, f"after 3 passes, step {i}")
+    plan.run(2)
+    x = np.asarray(wants[-1])
+    wants = _dependent_oracle(blocks, shapes, x, 2)
+    for i, (y, want) in enumerate(zip(ys, wants)):
+        assert_bytes_equal(host(y), want, f"after 3 + 2 passes, step {i}")
+    plan.close()
+
+
+def test_plan_several_launches_one_wait(gpu):
+    """Launches queue up; one wait covers them all; two plans share the queue."""
+    shapes_a = [(2048, 2048), (16384, 2048)]
+    shapes_b = [(2048, 8192), (3072, 2048)]
+    ma, xa, ya, wa = _independent(shapes_a, 1700)
+    mb, xb, yb, wb = _independent(shapes_b, 1800)
+    pa = Plan(gpu, _steps(ma, xa, ya, shapes_a), 2)
+    pb = Plan(gpu, _steps(mb, xb, yb, shapes_b), 2)
+    L = gpu.lib()
+    for _ in range(3):
+        gpu.check("launch a", L.w4a8_chain_plan_launch(pa.p, 2))
+        gpu.check("launch b", L.w4a8_chain_plan_launch(pb.p, 1))
+    gpu.check("wait b", L.w4a8_chain_plan_wait(pb.p, 30000))
+    gpu.check("wait a", L.w4a8_chain_plan_wait(pa.p, 30000))
+    for y, want in zip(ya + yb, wa + wb):
+        assert_bytes_equal(host(y), want, "queued launches")
+    pa.close()
+    pb.close()
+
+
+def test_plan_argument_checks(gpu):
+    L = gpu.lib()
+    shapes = [(64, 2048)]
+    mats, xs, ys, _ = _independent(shapes, 1900)
+    steps = _steps(mats, xs, ys, shapes)
+    p = ctypes.c_void_p()
+    assert L.w4a8_chain_plan_create(ctypes.cast(steps, ctypes.c_void_p), 0, ctypes.byref(p)) == -2
+    bad = _steps(mats, xs, ys, [(64, 1024)])         # k < 2048
+    assert L.w4a8_chain_plan_create(ctypes.cast(bad, ctypes.c_void_p), 1, ctypes.byref(p)) == -2
+    plan = Plan(gpu, steps, 1)
+    assert L.w4a8_chain_plan_launch(plan.p, 0) == -2
+    assert L.w4a8_chain_plan_wait(plan.p, 0) == 0       # nothing launched: done at once
+    plan.close()
