@@ -520,6 +520,7 @@ def cpu_baseline(chain, mats, xs, budget_s=30.0):
 
 
 def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph):
+    plan = not args.no_plan
     """The fields every bench line carries: the metric, the chain and its roofline."""
     n = len(cf.decode_chain())
     chain_bytes = cf.chain_algorithmic_bytes()
@@ -558,15 +559,19 @@ def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd
         "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("chain_traffic_bytes_per_launch"), "traffic_source": PMC_SUMMARY,
-                     "kernel": "w4a8_plan_gemv_f32 (gemv_m1_dev.h's fused Q8_0 quantize + GEMV), the chain "
-                               "plan's 65 dispatches",
+                     "kernel": ("w4a8_plan_gemv_f32 (gemv_m1_dev.h's fused Q8_0 quantize + GEMV), the chain "
+                                "plan's 65 dispatches" if plan else
+                                "gemv_m1_kernel<X_F32> (fused Q8_0 quantize + GEMV), w4a8_chain_gemv's 65 launches"),
                      "bytes_per_launch": round(chain_bytes / n), "us_per_launch": round(ms_per_step * 1e3 / n, 3),
-                     "timing": "host clock around the plan's timed launch and its wait, the device idle on both "
-                               "sides: step time / 65, dispatch boundaries included",
+                     "timing": ("host clock around the plan's timed launch and its wait, the device idle on both "
+                                "sides: step time / 65, dispatch boundaries included" if plan else
+                                "HIP events on the launch stream around the timed graph replays: step time / 65, "
+                                "launch boundaries included"),
                      "kernel_durations": kernel},
         "chain": {"us_per_step": round(ms_per_step * 1e3, 2), "gbps": round(chain_gbs, 1),
                   "hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4), "launches_per_step": n,
-                  "issued_by": "w4a8_chain_plan_launch (raw AQL dispatches, no cache fences between steps)",
+                  "issued_by": ("w4a8_chain_plan_launch (raw AQL dispatches, no cache fences between steps)"
+                                if plan else "w4a8_chain_gemv from a HIP graph"),
                   "verified": chain_check["ok"], "verification": chain_check,
                   "dependency": "matrix j+1 starts after matrix j's output is complete"},
         "chain_graph": graph,
@@ -577,7 +582,8 @@ def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd
 
 def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph):
     out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, pmc_traffic() or {}, graph)
-    out["mode"] = "chain only" + ("" if one_launch is None else " (plan, graph, then the one-launch chain)")
+    out["mode"] = "chain only: " + ("HIP graph" if args.no_plan else "plan, HIP graph") + (
+        "" if one_launch is None else ", one-launch chain")
     return out
 
 
@@ -616,6 +622,9 @@ def main() -> int:
                          "chain's kernel-trace profile is taken from")
     ap.add_argument("--no-one-launch", action="store_true",
                     help="skip the one-launch (cooperative) chain")
+    ap.add_argument("--no-plan", action="store_true",
+                    help="time the chain through w4a8_chain_gemv only (the headline then comes from the HIP "
+                         "graph): rocprofv3's kernel trace cannot follow the plan's own queue")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first copy MB of device memory once: a plain copy of known size whose "
                          "FETCH_SIZE / WRITE_SIZE counters scale the kernels' HBM traffic")
@@ -648,19 +657,22 @@ def main() -> int:
     ptr = ctypes.cast(steps, ctypes.c_void_p)
     chain_digests = [(r["name"], y, r["y"]) for y, r in zip(ys, recs)]
 
-    log(f"timing {args.steps} steps after {args.warmup} warm-up steps (chain plan)")
-    ms_per_step, wall = time_plan(torch, kv, L, ptr, n, args.steps, args.warmup, ys)
-    chain_check = verify(chain_digests)
-    chain_check["weights_ok"] = weights_ok
-    tok_s = 1e3 / ms_per_step
-    chain_gbs = chain_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"chain (plan): {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s, {chain_gbs:.0f} GB/s, "
-        f"outputs {'match' if chain_check['ok'] else 'DIFFER FROM'} the oracle's digests")
+    if not args.no_plan:
+        log(f"timing {args.steps} steps after {args.warmup} warm-up steps (chain plan)")
+        ms_per_step, wall = time_plan(torch, kv, L, ptr, n, args.steps, args.warmup, ys)
+        chain_check = verify(chain_digests)
+        chain_check["weights_ok"] = weights_ok
+        log(f"chain (plan): {ms_per_step * 1e3:.1f} us/step, {1e3 / ms_per_step:.0f} tokens/s, "
+            f"outputs {'match' if chain_check['ok'] else 'DIFFER FROM'} the oracle's digests")
 
     log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay of w4a8_chain_gemv)")
     g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
-    ms_graph, _ = time_replays(torch, stream, g_chain, args.steps, args.warmup, before=lambda: poison(ys))
+    ms_graph, wall_graph = time_replays(torch, stream, g_chain, args.steps, args.warmup, before=lambda: poison(ys))
     graph_check = verify(chain_digests)
+    if args.no_plan:
+        ms_per_step, wall, chain_check = ms_graph, wall_graph, dict(graph_check, weights_ok=weights_ok)
+    tok_s = 1e3 / ms_per_step
+    chain_gbs = chain_bytes / (ms_per_step * 1e-3) / 1e9
     graph = {"us_per_step": round(ms_graph * 1e3, 2), "tokens_per_s": round(1e3 / ms_graph, 1),
              "gbps": round(chain_bytes / (ms_graph * 1e-3) / 1e9, 1),
              "hbm_frac": round(chain_bytes / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "launches_per_step": n,

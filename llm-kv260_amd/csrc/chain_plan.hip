@@ -14,8 +14,10 @@
 // an output that a later step reads is written through to the device's
 // coherence point and waited for before its waves end, and that step reads
 // it from there (the kernels' _yc / _xc variants); everything else goes
-// through the caches as before. The kernel arguments sit in device memory,
-// written once when the plan is made.
+// through the caches as before. The kernel arguments sit in pinned,
+// coherent host memory, written once when the plan is made (as fast as
+// device memory here, 243-244 against 243 us per step, and readable by
+// tools that inspect a dispatch's arguments from the host).
 //
 // This mirrors how the reference drives its engine: the host starts the
 // work and later waits for it (board/kv260gemv/gemv2_dev.h:40-44,
@@ -38,7 +40,7 @@ struct w4a8_chain_plan {
     int n = 0;
     std::vector<int> kind;                 // kernel variant per step
     std::vector<uint32_t> grid, threads, group;
-    char *kargs = nullptr;                 // device memory, ARG_STRIDE bytes per step
+    char *kargs = nullptr;                 // pinned host memory, ARG_STRIDE bytes per step
     hsa_signal_t done{};                   // launches in flight
 };
 
@@ -199,16 +201,16 @@ int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out
     }
     std::vector<char> host((size_t)n * ARG_STRIDE, 0);
     for (int j = 0; j < n; ++j) std::memcpy(host.data() + (size_t)j * ARG_STRIDE, &args[j], sizeof(PlanArgs));
-    hipError_t e = hipMalloc(&p->kargs, host.size());
-    if (e == hipSuccess) e = hipMemcpy(p->kargs, host.data(), host.size(), hipMemcpyHostToDevice);
+    hipError_t e = hipHostMalloc(&p->kargs, host.size(), hipHostMallocCoherent);
+    if (e == hipSuccess) std::memcpy(p->kargs, host.data(), host.size());
     if (e != hipSuccess) {
-        if (p->kargs) (void)hipFree(p->kargs);
+        if (p->kargs) (void)hipHostFree(p->kargs);
         delete p;
         he = e;
         return W4A8_ERR_HIP;
     }
     if (hsa_signal_create(0, 0, nullptr, &p->done) != HSA_STATUS_SUCCESS) {
-        (void)hipFree(p->kargs);
+        (void)hipHostFree(p->kargs);
         delete p;
         return W4A8_ERR_HSA;
     }
@@ -276,7 +278,7 @@ int chain_plan_destroy(w4a8_chain_plan *p) {
     const int s = chain_plan_wait(p, 10000);
     if (s != W4A8_OK) return s;   // work in flight: the plan stays valid
     hsa_signal_destroy(p->done);
-    (void)hipFree(p->kargs);
+    (void)hipHostFree(p->kargs);
     delete p;
     return W4A8_OK;
 }
