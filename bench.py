@@ -624,7 +624,7 @@ def main() -> int:
                     help="skip the one-launch (cooperative) chain")
     ap.add_argument("--no-plan", action="store_true",
                     help="time the chain through w4a8_chain_gemv only (the headline then comes from the HIP "
-                         "graph): rocprofv3's kernel trace cannot follow the plan's own queue")
+                         "graph)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first copy MB of device memory once: a plain copy of known size whose "
                          "FETCH_SIZE / WRITE_SIZE counters scale the kernels' HBM traffic")

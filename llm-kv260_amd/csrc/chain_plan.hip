@@ -257,8 +257,13 @@ int chain_plan_launch(w4a8_chain_plan *p, int passes) {
                        ((last ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_NONE) << HSA_PACKET_HEADER_SCRELEASE_FENCE_SCOPE));
         const uint32_t setup = 1u << HSA_KERNEL_DISPATCH_PACKET_SETUP_DIMENSIONS;
         __atomic_store_n(&pk->full_header, (uint32_t)header | (setup << 16), __ATOMIC_RELEASE);
-        // Ring once per pass, so the device starts while later passes are written.
-        if (j == p->n - 1) hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
+        // Ring once per pass, so the device starts while later passes are
+        // written, and at the ring's last slot, so that no rung range of
+        // packets wraps around the ring's end (a queue interceptor, such as a
+        // profiler's, may copy a rung range as one block: with ranges that
+        // wrapped, rocprofv3's kernel trace read past the ring and crashed).
+        if (j == p->n - 1 || ((idx + 1) & (q->size - 1)) == 0)
+            hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
     }
     return W4A8_OK;
 }
