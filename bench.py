@@ -366,10 +366,59 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu
     gr = graph_of(torch, stream, checked)
     ms, _ = time_replays(torch, stream, gr, steps, warmup)
     del gr
-    return {"us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "launches_per_step": len(calls),
-            "gbps": round(cf.chain_algorithmic_bytes() / (ms * 1e-3) / 1e9, 1),
-            "silu": "gate|up epilogue" if silu_epilogue else "down's staging",
-            "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
+    out = {"us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "launches_per_step": len(calls),
+           "gbps": round(cf.chain_algorithmic_bytes() / (ms * 1e-3) / 1e9, 1),
+           "silu": "gate|up epilogue" if silu_epilogue else "down's staging",
+           "issued_by": "the stream entry points from a HIP graph",
+           "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
+    if not silu_epilogue:
+        return out
+    # The same steps as a chain plan (w4a8_chain_plan_create_steps), then its
+    # outputs and pick against the graph's, byte for byte.
+    torch.cuda.synchronize()
+    ref = [y.clone() for y in ys] + [best.clone()]
+    S, plan_steps = kv.PlanStep, []
+    for i, m in enumerate(chain):
+        w, y = mats[i], ys[i]
+        role = "lm" if i == len(chain) - 1 else ("qkv", "o", "gate_up", "down")[i % 4]
+        if role == "gate_up":
+            plan_steps.append(S(kv.PLAN_GATE_UP_SILU, w.data_ptr(), resid.data_ptr(), y.data_ptr(), m.rows, m.k,
+                                norm.data_ptr(), 1e-5))
+        elif role == "down":
+            plan_steps.append(S(kv.PLAN_GEMV, w.data_ptr(), ys[i - 1].data_ptr(), y.data_ptr(), m.rows, m.k, None, 0.0))
+        elif role == "qkv":
+            plan_steps.append(S(kv.PLAN_GEMV, w.data_ptr(), resid.data_ptr(), y.data_ptr(), m.rows, m.k,
+                                norm.data_ptr(), 1e-5))
+        elif role == "o":
+            plan_steps.append(S(kv.PLAN_GEMV, w.data_ptr(), attn.data_ptr(), y.data_ptr(), m.rows, m.k, None, 0.0))
+        else:
+            plan_steps.append(S(kv.PLAN_ARGMAX, w.data_ptr(), resid.data_ptr(), y.data_ptr(), m.rows, m.k,
+                                norm.data_ptr(), 1e-5, best.data_ptr(), ws.data_ptr()))
+    arr = (S * len(plan_steps))(*plan_steps)
+    plan = ctypes.c_void_p()
+    kv.check("w4a8_chain_plan_create_steps",
+             L.w4a8_chain_plan_create_steps(ctypes.cast(arr, ctypes.c_void_p), len(plan_steps), ctypes.byref(plan)))
+    try:
+        kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, max(warmup, 1)))
+        kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
+        poison(ys)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, steps))
+        kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 120000))
+        dt = time.perf_counter() - t0
+        torch.cuda.synchronize()
+    finally:
+        kv.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
+    # gate|up with the silu epilogue writes rows/2 values (silu(gate) * up);
+    # the rest of its output buffer is not an output.
+    written = [y[:m.rows // 2] if i % 4 == 2 and i != len(chain) - 1 else y for i, (m, y) in enumerate(zip(chain, ys))]
+    same = all(torch.equal(a.view(torch.int32), b[:a.numel()].view(torch.int32))
+               for a, b in zip(written + [best], ref))
+    out["plan"] = {"us_per_step": round(dt * 1e6 / steps, 2), "tokens_per_s": round(steps / dt, 1),
+                   "issued_by": "w4a8_chain_plan_create_steps / _launch / _wait",
+                   "verified": same, "verification": "every output and the picked row equal the graph's"}
+    return out
 
 
 def time_prefill(torch, kv, cf, chain, mats, stream, mrows, reps=5):
@@ -725,7 +774,8 @@ def main() -> int:
     fused_chain["silu_in_down_staging_us_per_step"] = staged["us_per_step"]
     log(f"fused chain: {fused_chain['us_per_step']} us/step, {fused_chain['tokens_per_s']} tokens/s "
         f"(rmsnorm fused, silu in gate|up's epilogue, LM head with argmax); {staged['us_per_step']} us/step "
-        "with silu in down's staging")
+        f"with silu in down's staging; as a chain plan {fused_chain['plan']['us_per_step']} us/step, "
+        f"verified {fused_chain['plan']['verified']}")
 
     gemv, gemm = {}, []
     shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES
@@ -768,12 +818,14 @@ def main() -> int:
         log("CPU baseline (bounded sample)")
         cpu = cpu_baseline(chain, mats, xs)
     verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and graph["verified"] and
+                fused_chain["plan"]["verified"] and
                 (one_launch is None or one_launch["verified"]) and
                 all(r["verified"] for r in gemm) and prefill[0]["verified"] is True)
 
     out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph)
     out["verified"] = verified
     out["verification"] = {"chain": chain_check, "chain_graph": graph_check, "batch": batch_check,
+                           "fused_chain_plan": fused_chain["plan"]["verified"],
                            "one_launch": one_launch["verified"] if one_launch else None,
                            "gemm": {f"{r['name']} M={r['m']}": r["verified"] for r in gemm},
                            "prefill24": prefill[0]["verification"],

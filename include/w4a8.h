@@ -257,6 +257,38 @@ int w4a8_chain_timeouts(void);
  * Launches of plans on one device go to that device's queue in call order. */
 typedef struct w4a8_chain_plan w4a8_chain_plan;
 int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan);
+
+/* A plan whose steps may carry the producers either side of the GEMV, each
+ * step byte-identical to the stream entry point it names:
+ *   W4A8_PLAN_GEMV            w4a8_gemv_f32, or w4a8_gemv_rmsnorm when
+ *                             norm_w is set (k <= 8192);
+ *   W4A8_PLAN_GATE_UP_SILU    w4a8_gemv_gate_up_silu: y = silu(gate) * up,
+ *                             float32[rows / 2] (its shape rules);
+ *   W4A8_PLAN_ARGMAX          w4a8_gemv_f32_argmax, or w4a8_gemv_rmsnorm_argmax
+ *                             when norm_w is set: *argmax = the row picked,
+ *                             through `workspace` (w4a8_argmax_workspace_bytes(),
+ *                             zero before the first launch; the step leaves
+ *                             it zero).
+ * Every k in 2048..W4A8_MAX_K; the rest as w4a8_chain_plan_create (which is
+ * this with every step a W4A8_PLAN_GEMV without norm_w). A step may read an
+ * earlier (or, over passes, a later) step's y; norm_w, argmax and the
+ * workspace must not be another step's y. */
+#define W4A8_PLAN_GEMV 0
+#define W4A8_PLAN_GATE_UP_SILU 1
+#define W4A8_PLAN_ARGMAX 2
+typedef struct w4a8_plan_step {
+    int kind;
+    const void *w;          /* Q4_0 rows, 16-byte aligned */
+    const float *x;         /* float32[k], 16-byte aligned */
+    float *y;               /* float32[rows] (gate|up: [rows / 2]) */
+    int rows;
+    int k;
+    const float *norm_w;    /* float32[k], 16-byte aligned, or NULL */
+    float eps;
+    int32_t *argmax;        /* W4A8_PLAN_ARGMAX only */
+    void *workspace;        /* W4A8_PLAN_ARGMAX only, 16-byte aligned */
+} w4a8_plan_step;
+int w4a8_chain_plan_create_steps(const w4a8_plan_step *steps, int n, w4a8_chain_plan **plan);
 int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes);
 int w4a8_chain_plan_wait(w4a8_chain_plan *plan, int timeout_ms);
 int w4a8_chain_plan_destroy(w4a8_chain_plan *plan);

@@ -224,17 +224,39 @@ int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream) {
     return hip_status(launch_chain(steps, n, (hipStream_t)stream));
 }
 
+int w4a8_chain_plan_create_steps(const w4a8_plan_step *steps, int n, w4a8_chain_plan **plan) {
+    if (!steps || !plan) return W4A8_ERR_NULL;
+    *plan = nullptr;
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
+    // The checks of the stream entry point each step stands for.
+    for (int i = 0; i < n; ++i) {
+        const w4a8_plan_step &s = steps[i];
+        if (int st = check_gemv(s.w, s.x, s.y, s.rows, s.k, 16)) return st;
+        if (s.k < 2048 || s.kind < W4A8_PLAN_GEMV || s.kind > W4A8_PLAN_ARGMAX) return W4A8_ERR_SHAPE;
+        if (s.norm_w) {
+            if (s.k > RMS_FUSED_MAX_K) return W4A8_ERR_SHAPE;
+            if (!aligned(s.norm_w, 16)) return W4A8_ERR_ALIGN;
+        }
+        if (s.kind == W4A8_PLAN_GATE_UP_SILU && gate_up_silu_waves(s.rows, s.k) == 0) return W4A8_ERR_SHAPE;
+        if (s.kind == W4A8_PLAN_ARGMAX) {
+            if (!s.argmax || !s.workspace) return W4A8_ERR_NULL;
+            if (!aligned(s.argmax, 4) || !aligned(s.workspace, 16)) return W4A8_ERR_ALIGN;
+        }
+    }
+    hipError_t he = hipSuccess;
+    const int st = chain_plan_create(steps, n, plan, he);
+    return st == W4A8_ERR_HIP ? hip_status(he) : st;
+}
+
 int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan) {
     if (!steps || !plan) return W4A8_ERR_NULL;
     *plan = nullptr;
     if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
-    for (int i = 0; i < n; ++i) {
-        if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
-        if (steps[i].k < 2048) return W4A8_ERR_SHAPE;
-    }
-    hipError_t he = hipSuccess;
-    const int s = chain_plan_create(steps, n, plan, he);
-    return s == W4A8_ERR_HIP ? hip_status(he) : s;
+    w4a8_plan_step ps[W4A8_CHAIN_MAX_STEPS] = {};
+    for (int i = 0; i < n; ++i)
+        ps[i] = w4a8_plan_step{W4A8_PLAN_GEMV, steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k,
+                               nullptr, 0.0f, nullptr, nullptr};
+    return w4a8_chain_plan_create_steps(ps, n, plan);
 }
 
 int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes) {

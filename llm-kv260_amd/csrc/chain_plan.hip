@@ -1,7 +1,8 @@
-// The decode step's GEMV chain as a plan: the per-step chain's kernel
-// (gemv_m1_dev.h, fp32 x quantized in its staging), dispatched as raw AQL
-// packets on an HSA queue of the library's own (one per device) instead of
-// through HIP launches.
+// The decode step's GEMV chain as a plan: the M = 1 GEMV's kernels
+// (gemv_m1_dev.h, fp32 x quantized in their staging; with the rmsnorm, the
+// silu * up epilogue or the greedy pick fused as the stream entry points
+// have them), dispatched as raw AQL packets on an HSA queue of the library's
+// own (one per device) instead of through HIP launches.
 //
 // Why: between two kernels of a HIP stream or graph the packet processor
 // runs a release fence (every XCD's L2 written back) and an acquire fence
@@ -26,6 +27,7 @@
 #include <hsa/hsa_ext_amd.h>
 
 #include <chrono>
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -58,8 +60,12 @@ struct PlanArgs {
 static_assert(sizeof(PlanArgs) == 176, "argument block of the plan's kernels");
 constexpr size_t ARG_STRIDE = 256;
 constexpr uint32_t QUEUE_PACKETS = 16384;
-constexpr const char *KERNEL_NAMES[4] = {"w4a8_plan_gemv_f32.kd", "w4a8_plan_gemv_f32_xc.kd", "w4a8_plan_gemv_f32_yc.kd",
-                                         "w4a8_plan_gemv_f32_xyc.kd"};
+// Kernel variants: (step kind) x (x as is, or rmsnorm first) x (coherence),
+// in chain_plan_kernels.hip, w4a8_plan_<kind>_<format><coherence>.
+constexpr int N_KINDS = 3, N_KERNELS = N_KINDS * 2 * 4;
+constexpr const char *KIND_NAMES[N_KINDS] = {"gemv", "pair", "argmax"};
+constexpr const char *COH_NAMES[4] = {"", "_xc", "_yc", "_xyc"};
+constexpr int kernel_index(int kind, bool rms, int coh) { return (kind * 2 + (rms ? 1 : 0)) * 4 + coh; }
 constexpr double QUEUE_SPACE_WAIT_S = 10.0;    // bound on waiting for free packet slots
 
 struct DeviceRuntime {
@@ -69,8 +75,8 @@ struct DeviceRuntime {
     hsa_agent_t agent{};
     hsa_queue_t *queue = nullptr;
     hsa_executable_t exe{};
-    uint64_t kobj[4]{};
-    uint32_t group[4]{}, priv[4]{};
+    uint64_t kobj[N_KERNELS]{};
+    uint32_t group[N_KERNELS]{}, priv[N_KERNELS]{};
 };
 constexpr int MAX_DEVICES = 16;
 DeviceRuntime g_rt[MAX_DEVICES];
@@ -127,9 +133,12 @@ int runtime_of(int dev, DeviceRuntime *&out) {
         hsa_executable_load_agent_code_object(rt.exe, rt.agent, rd, nullptr, nullptr) != HSA_STATUS_SUCCESS ||
         hsa_executable_freeze(rt.exe, nullptr) != HSA_STATUS_SUCCESS)
         return rt.status;
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < N_KERNELS; ++v) {
         hsa_executable_symbol_t sym;
-        if (hsa_executable_get_symbol_by_name(rt.exe, KERNEL_NAMES[v], &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
+        char name[64];
+        std::snprintf(name, sizeof name, "w4a8_plan_%s_%s%s.kd", KIND_NAMES[v / 8], (v / 4) % 2 ? "rms" : "f32",
+                      COH_NAMES[v % 4]);
+        if (hsa_executable_get_symbol_by_name(rt.exe, name, &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
             hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &rt.kobj[v]) !=
                 HSA_STATUS_SUCCESS ||
             hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE, &rt.group[v]) !=
@@ -151,7 +160,7 @@ bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
 
 }  // namespace
 
-int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out, hipError_t &he) {
+int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out, hipError_t &he) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return W4A8_ERR_NODEV;
     DeviceRuntime *rt = nullptr;
@@ -160,19 +169,34 @@ int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out
     p->device = dev;
     p->n = n;
     p->kind.assign(n, 0);
-    // Which outputs another step reads, in this pass or the next.
+    // Which outputs another step reads, in this pass or the next (gate|up's
+    // output is its rows / 2 products).
+    auto y_bytes = [&](const w4a8_plan_step &s) {
+        return 4 * (size_t)(s.kind == W4A8_PLAN_GATE_UP_SILU ? s.rows / 2 : s.rows);
+    };
+    std::vector<int> coh(n, 0);
     for (int j = 0; j < n; ++j)
         for (int i = 0; i < n; ++i)
-            if (overlaps(steps[j].x, 4 * (size_t)steps[j].k, steps[i].y, 4 * (size_t)steps[i].rows)) {
-                p->kind[j] |= COH_X;
-                p->kind[i] |= COH_Y;
+            if (overlaps(steps[j].x, 4 * (size_t)steps[j].k, steps[i].y, y_bytes(steps[i]))) {
+                coh[j] |= COH_X;
+                coh[i] |= COH_Y;
             }
     const int cus = device_cu_count();
     std::vector<PlanArgs> args(n);
     for (int j = 0; j < n; ++j) {
-        const w4a8_chain_step &s = steps[j];
+        const w4a8_plan_step &s = steps[j];
+        const bool rms = s.norm_w != nullptr;
+        const XFormat xf = rms ? X_RMS : X_F32;
+        p->kind[j] = kernel_index(s.kind, rms, coh[j]);
         const int C = s.k / 256, rpw = 64 / C, tiles = (s.rows + rpw - 1) / rpw;
-        const M1Shape sh = gemv_m1_shape(tiles, s.k, X_F32, false, cus);
+        M1Shape sh = gemv_m1_shape(tiles, s.k, xf, s.kind == W4A8_PLAN_ARGMAX, cus);
+        if (s.kind == W4A8_PLAN_GATE_UP_SILU) {
+            // gate|up's shape (launch_gemv_gate_up_silu): tiles / 2 waves, rows r and r + rows / 2 per wave.
+            const int waves = gate_up_silu_waves(s.rows, s.k);
+            sh.grid = tiles / 2 / waves;
+            sh.threads = 64 * waves;
+            sh.lds = (size_t)waves * TILE_BYTES + x_lds_bytes(s.k / QK) + (rms ? rms_sq_doubles(s.k) * 8 + 16 : 0);
+        }
         PlanArgs a;
         std::memset(&a, 0, sizeof a);
         a.w0 = static_cast<const uint8_t *>(s.w);
@@ -194,6 +218,13 @@ int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out
         a.P.C = C;
         a.P.rpw = rpw;
         a.P.tiles = tiles;
+        a.P.norm_w = s.norm_w;
+        a.P.eps = s.eps;
+        if (s.kind == W4A8_PLAN_ARGMAX) {
+            a.P.argmax = s.argmax;
+            a.P.ticket = static_cast<unsigned int *>(s.workspace);
+            a.P.key = reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(s.workspace) + ARGMAX_KEY_OFFSET);
+        }
         args[j] = a;
         p->grid.push_back((uint32_t)sh.grid);
         p->threads.push_back((uint32_t)sh.threads);

@@ -1,10 +1,12 @@
 // The chain plan's code object (chain_plan.hip dispatches these kernels as
-// raw AQL packets): the per-step chain's M = 1 GEMV with the fp32 activation
-// quantized in its staging (gemv_m1_dev.h, the same body, byte for byte), in
-// four coherence variants and under plain C names. A plan's dispatches carry
-// no cache fences between them, so a step whose x an earlier step wrote reads
-// it from the device's coherence point (_xc), and a step whose y a later step
-// reads writes it through (_yc); the others use the caches as usual.
+// raw AQL packets): the M = 1 GEMV with its fp32 activation quantized in its
+// staging (gemv_m1_dev.h, the same body, byte for byte), with or without the
+// rmsnorm before it, as a plain GEMV, as gate|up with silu * up as its
+// epilogue and as the LM head with its greedy pick, each in four coherence
+// variants and under plain C names. A plan's dispatches carry no cache fences
+// between them, so a step whose x an earlier step wrote reads it from the
+// device's coherence point (_xc), and a step whose y a later step reads
+// writes it through (_yc); the others use the caches as usual.
 // Built as a device-only code object and embedded in the library
 // (chain_plan_co.S); not linked as a HIP module.
 #include "gemv_m1_dev.h"
@@ -12,7 +14,7 @@
 namespace w4a8 {
 namespace {
 
-template <int COH>
+template <int XF, bool ARGMAX, bool PAIR, int COH>
 __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int rows, int k, int C, int rpw, int tiles,
                                           int nblocks, int nthreads, GemvParams &P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -23,7 +25,7 @@ __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int 
     P.C = C;
     P.rpw = rpw;
     P.tiles = tiles;
-    gemv_m1_body<X_F32, true, true, false, false, COH>(P, blockIdx.x, nblocks, nthreads, lds);
+    gemv_m1_body<XF, true, true, ARGMAX, PAIR, COH>(P, blockIdx.x, nblocks, nthreads, lds);
 }
 
 }  // namespace
@@ -36,15 +38,24 @@ __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int 
         w4a8::GemvParams P
 #define W4A8_PLAN_PASS w0, x, rows, k, C, rpw, tiles, nblocks, nthreads, P
 
-extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void w4a8_plan_gemv_f32(W4A8_PLAN_ARGS) {
-    w4a8::plan_step<0>(W4A8_PLAN_PASS);
-}
-extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void w4a8_plan_gemv_f32_xc(W4A8_PLAN_ARGS) {
-    w4a8::plan_step<w4a8::COH_X>(W4A8_PLAN_PASS);
-}
-extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void w4a8_plan_gemv_f32_yc(W4A8_PLAN_ARGS) {
-    w4a8::plan_step<w4a8::COH_Y>(W4A8_PLAN_PASS);
-}
-extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void w4a8_plan_gemv_f32_xyc(W4A8_PLAN_ARGS) {
-    w4a8::plan_step<w4a8::COH_X | w4a8::COH_Y>(W4A8_PLAN_PASS);
-}
+// One kernel per (step kind, activation format, coherence variant), named
+// w4a8_plan_<kind>_<format><variant>; chain_plan.hip builds the same names.
+#define W4A8_PLAN_KERNEL(NAME, XF, ARGMAX, PAIR, COH)                                          \
+    extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void NAME(W4A8_PLAN_ARGS) { \
+        w4a8::plan_step<XF, ARGMAX, PAIR, COH>(W4A8_PLAN_PASS);                                \
+    }
+#define W4A8_PLAN_KIND(KIND, FMT, XF, ARGMAX, PAIR)                                            \
+    W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT, XF, ARGMAX, PAIR, 0)                            \
+    W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT##_xc, XF, ARGMAX, PAIR, w4a8::COH_X)             \
+    W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT##_yc, XF, ARGMAX, PAIR, w4a8::COH_Y)             \
+    W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT##_xyc, XF, ARGMAX, PAIR, w4a8::COH_X | w4a8::COH_Y)
+
+// The GEMV (w4a8_gemv_f32, w4a8_gemv_rmsnorm), gate|up with silu * up as its
+// epilogue (w4a8_gemv_gate_up_silu), the LM head with its greedy pick
+// (w4a8_gemv_f32_argmax, w4a8_gemv_rmsnorm_argmax).
+W4A8_PLAN_KIND(gemv, f32, w4a8::X_F32, false, false)
+W4A8_PLAN_KIND(gemv, rms, w4a8::X_RMS, false, false)
+W4A8_PLAN_KIND(pair, f32, w4a8::X_F32, false, true)
+W4A8_PLAN_KIND(pair, rms, w4a8::X_RMS, false, true)
+W4A8_PLAN_KIND(argmax, f32, w4a8::X_F32, true, false)
+W4A8_PLAN_KIND(argmax, rms, w4a8::X_RMS, true, false)

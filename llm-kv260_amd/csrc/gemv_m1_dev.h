@@ -216,9 +216,9 @@ __device__ __forceinline__ void load_tile(const GemvParams &P, int tile, int lan
 // No fence is needed (an agent-scope release or acquire would write back or
 // invalidate the whole L2 of every XCD in turn). The last workgroup writes the
 // row and clears the key and the ticket for the next call.
-__device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long long best, int nblocks,
+__device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long long best, int nblocks, int waves,
                                               uint8_t *lds) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     unsigned long long *keys = reinterpret_cast<unsigned long long *>(lds);   // the slabs are free by now
     best = wave_max_u64(best);
     __syncthreads();
@@ -250,7 +250,8 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
 // COH (the chain plan's dispatches, which carry no cache fences between
 // them): bit 0, x is an earlier step's output, read from the device's
 // coherence point (past the L2 of this XCD); bit 1, y is a later step's x,
-// written through to it and waited for before the wave ends. ONE_PASS only.
+// written through to it and waited for before the wave ends. ONE_PASS (and
+// PAIR) only; fp32 x formats only.
 constexpr int COH_X = 1, COH_Y = 2;
 
 template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false, int COH = 0>
@@ -392,7 +393,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
             held = up ? held : yv;
             const float act = silu_mul(held, yv);
-            store_y(y_rsrc, up && mine ? 4 * (row - (P.rows >> 1)) : OUT_OF_RANGE, act);
+            store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, up && mine ? 4 * (row - (P.rows >> 1)) : OUT_OF_RANGE, act);
         } else if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
             const int row = row_of(acc_r);
@@ -441,7 +442,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     } else {
         stage_x();
     }
-    if constexpr (ARGMAX) argmax_finish(P, best, nblocks, lds);
+    if constexpr (ARGMAX) argmax_finish(P, best, nblocks, waves, lds);
     if constexpr ((COH & COH_Y) != 0) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 

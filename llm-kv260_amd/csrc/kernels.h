@@ -101,6 +101,7 @@ hipError_t launch_silu_mul_q8_0(const float *gate_up, int k, int m, uint8_t *out
 
 struct w4a8_chain_step;   // include/w4a8.h
 struct w4a8_chain_plan;   // chain_plan.hip
+struct w4a8_plan_step;    // include/w4a8.h
 
 namespace w4a8 {
 
@@ -112,7 +113,7 @@ bool chain_one_launch_fits(const w4a8_chain_step *steps, int n);
 hipError_t launch_chain_one(const w4a8_chain_step *steps, int n, hipStream_t stream);
 // The chain plan (chain_plan.hip): statuses as the C ABI's; a HIP error of
 // create comes back in `he` with W4A8_ERR_HIP.
-int chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **out, hipError_t &he);
+int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out, hipError_t &he);
 int chain_plan_launch(w4a8_chain_plan *p, int passes);
 int chain_plan_wait(w4a8_chain_plan *p, int timeout_ms);
 int chain_plan_destroy(w4a8_chain_plan *p);

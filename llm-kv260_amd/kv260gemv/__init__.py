@@ -43,7 +43,8 @@ EXPORTS = (
     "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
     "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk", "w4a8_topk_no_alloc", "w4a8_gemv_gate_up_silu",
     "w4a8_chain_set_mode", "w4a8_chain_set_spin_limit", "w4a8_chain_timeouts",
-    "w4a8_chain_plan_create", "w4a8_chain_plan_launch", "w4a8_chain_plan_wait", "w4a8_chain_plan_destroy",
+    "w4a8_chain_plan_create", "w4a8_chain_plan_create_steps", "w4a8_chain_plan_launch", "w4a8_chain_plan_wait",
+    "w4a8_chain_plan_destroy",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -134,8 +135,9 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).restype = i
     L.w4a8_chain_timeouts.argtypes = []
     L.w4a8_chain_timeouts.restype = i
-    L.w4a8_chain_plan_create.argtypes = [p, i, ctypes.POINTER(p)]
-    L.w4a8_chain_plan_create.restype = i
+    for f in ("w4a8_chain_plan_create", "w4a8_chain_plan_create_steps"):
+        getattr(L, f).argtypes = [p, i, ctypes.POINTER(p)]
+        getattr(L, f).restype = i
     for f in ("w4a8_chain_plan_launch", "w4a8_chain_plan_wait"):
         getattr(L, f).argtypes = [p, i]
         getattr(L, f).restype = i
@@ -143,6 +145,16 @@ def lib() -> ctypes.CDLL:
     L.w4a8_chain_plan_destroy.restype = i
     _lib = L
     return L
+
+
+PLAN_GEMV, PLAN_GATE_UP_SILU, PLAN_ARGMAX = 0, 1, 2
+
+
+class PlanStep(ctypes.Structure):
+    """include/w4a8.h's w4a8_plan_step."""
+    _fields_ = [("kind", ctypes.c_int), ("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("rows", ctypes.c_int), ("k", ctypes.c_int), ("norm_w", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("argmax", ctypes.c_void_p), ("workspace", ctypes.c_void_p)]
 
 
 def strerror(status: int) -> str:

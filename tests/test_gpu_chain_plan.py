@@ -185,3 +185,94 @@ def test_plan_argument_checks(gpu):
     assert L.w4a8_chain_plan_launch(plan.p, 0) == -2
     assert L.w4a8_chain_plan_wait(plan.p, 0) == 0       # nothing launched: done at once
     plan.close()
+
+
+# ------------------------------------------------------------- producers
+
+
+def _blocks(rows, k, seed):
+    return dev(C.quantize_q4_0(O.normal_f32((rows, k), seed, 0.02)))
+
+
+def _run_steps(gpu, steps, passes):
+    import torch
+    L = gpu.lib()
+    arr = (gpu.PlanStep * len(steps))(*steps)
+    torch.cuda.synchronize()
+    p = ctypes.c_void_p()
+    gpu.check("w4a8_chain_plan_create_steps", L.w4a8_chain_plan_create_steps(ctypes.cast(arr, ctypes.c_void_p),
+                                                                             len(steps), ctypes.byref(p)))
+    gpu.check("launch", L.w4a8_chain_plan_launch(p, passes))
+    gpu.check("wait", L.w4a8_chain_plan_wait(p, 30000))
+    gpu.check("destroy", L.w4a8_chain_plan_destroy(p))
+
+
+def test_plan_producer_steps_match_the_stream_entry_points(gpu):
+    """A decode step with its producers: q|k|v and gate|up read rmsnorm(x),
+    down reads gate|up's silu * up output, the LM head picks its row; the same
+    steps without the rmsnorm. Every output and the picked row against the
+    stream entry points, over two passes."""
+    import torch
+    k, n_ff, vocab = 2048, 8192, 20000
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    resid = torch.randn(k, generator=g, device="cuda")
+    attn = torch.randn(k, generator=g, device="cuda")
+    norm = torch.randn(k, generator=g, device="cuda")
+    W = {"qkv": _blocks(3072, k, 11), "o": _blocks(k, k, 12), "gu": _blocks(2 * n_ff, k, 13),
+         "down": _blocks(k, n_ff, 14), "lm": _blocks(vocab, k, 15)}
+    for with_norm in (True, False):
+        nw = norm if with_norm else None
+        # the stream entry points
+        want_qkv = (gpu.gemv_rmsnorm(W["qkv"], k, resid, norm, 1e-5) if with_norm
+                    else gpu.gemv_q4_0_f32(W["qkv"], k, resid))
+        want_o = gpu.gemv_q4_0_f32(W["o"], k, attn)
+        want_act = gpu.gemv_gate_up_silu(W["gu"], k, resid, nw, 1e-5)
+        want_down = gpu.gemv_q4_0_f32(W["down"], n_ff, want_act)
+        ws0 = gpu.argmax_workspace()
+        want_lm, want_pick = (gpu.gemv_rmsnorm_argmax(W["lm"], k, resid, norm, 1e-5, ws0) if with_norm
+                              else gpu.gemv_q4_0_f32_argmax(W["lm"], k, resid, ws0))
+        torch.cuda.synchronize()
+        # the plan
+        ys = {"qkv": poisoned_f32(3072), "o": poisoned_f32(k), "act": poisoned_f32(n_ff), "down": poisoned_f32(k),
+              "lm": poisoned_f32(vocab)}
+        pick = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+        ws = gpu.argmax_workspace()
+        nptr = norm.data_ptr() if with_norm else None
+        S = gpu.PlanStep
+        steps = [S(gpu.PLAN_GEMV, W["qkv"].data_ptr(), resid.data_ptr(), ys["qkv"].data_ptr(), 3072, k, nptr, 1e-5),
+                 S(gpu.PLAN_GEMV, W["o"].data_ptr(), attn.data_ptr(), ys["o"].data_ptr(), k, k, None, 0.0),
+                 S(gpu.PLAN_GATE_UP_SILU, W["gu"].data_ptr(), resid.data_ptr(), ys["act"].data_ptr(), 2 * n_ff, k,
+                   nptr, 1e-5),
+                 S(gpu.PLAN_GEMV, W["down"].data_ptr(), ys["act"].data_ptr(), ys["down"].data_ptr(), k, n_ff,
+                   None, 0.0),
+                 S(gpu.PLAN_ARGMAX, W["lm"].data_ptr(), resid.data_ptr(), ys["lm"].data_ptr(), vocab, k, nptr, 1e-5,
+                   pick.data_ptr(), ws.data_ptr())]
+        _run_steps(gpu, steps, 2)
+        tag = "rmsnorm" if with_norm else "plain"
+        for name, want in (("qkv", want_qkv), ("o", want_o), ("act", want_act), ("down", want_down),
+                           ("lm", want_lm)):
+            assert_bytes_equal(host(ys[name]), host(want), f"{tag}: {name}")
+        assert int(pick.item()) == int(want_pick.item()), f"{tag}: picked row"
+        assert not ws.any().item(), "the argmax step leaves its workspace zero"
+
+
+def test_plan_steps_argument_checks(gpu):
+    import torch
+    L = gpu.lib()
+    S = gpu.PlanStep
+    w = _blocks(64, 2048, 21)
+    x = torch.zeros(2048, device="cuda")
+    y = torch.zeros(64, device="cuda")
+    p = ctypes.c_void_p()
+
+    def create(step):
+        arr = (S * 1)(step)
+        return L.w4a8_chain_plan_create_steps(ctypes.cast(arr, ctypes.c_void_p), 1, ctypes.byref(p))
+    assert create(S(7, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 2048, None, 0.0)) == -2       # kind
+    assert create(S(gpu.PLAN_ARGMAX, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 2048, None, 0.0)) == -1
+    assert create(S(gpu.PLAN_GATE_UP_SILU, w.data_ptr(), x.data_ptr(), y.data_ptr(), 6, 2048, None, 0.0)) == -2
+    w16 = _blocks(64, 16384, 22)
+    x16 = torch.zeros(16384, device="cuda")
+    assert create(S(gpu.PLAN_GEMV, w16.data_ptr(), x16.data_ptr(), y.data_ptr(), 64, 16384, x16.data_ptr(),
+                    1e-5)) == -2                                                                  # rmsnorm k > 8192
