@@ -187,55 +187,87 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // 1 / sqrtf((float)(ss / n) + eps).
 //
 // Layout: chain c's squares lie contiguously, square i at rms_sq_index(i, n),
-// each chain n / 4 + 2 doubles after the last (a chain stride of 2 mod 32
-// doubles puts the four chains' 16-byte reads in distinct banks);
-// rms_sq_doubles(n) doubles in all, 16-byte aligned. The squares are written
-// by the whole workgroup beforehand, so the chains carry the adds and
-// nothing else: lane c of the calling wave runs chain c, two squares per
-// 16-byte read, the next four reads in flight while the current eight
-// squares are added. The result is returned in every lane of the wave.
+// each chain n / 4 + 2 doubles after the last; rms_sq_doubles(n) doubles in
+// all, 16-byte aligned. The squares are written by the whole workgroup
+// beforehand, so the chains carry the adds and nothing else.
+//
+// One wave runs the four chains, chain c in row c (lanes 16c .. 16c + 15):
+// lane 16c + i holds chain c's squares 16g + i, g = 0, 1, ..., one 8-byte LDS
+// read per lane per sixteen steps, four reads ahead. Each step is one
+// v_fmac_f64 whose first operand comes through DPP row_newbcast:i (lane i of
+// the row, to every lane of it): acc = sq * 1.0 + acc, the chain's add
+// exactly (the product is exact, the fma rounds once). So a step costs one
+// dependent float64 instruction (about 5.4 clocks at n = 2048: 2,764 for 512
+// steps, where a chain lane reading its own squares from LDS took 4,900-6,300).
+// The whole wave must be active. The result is returned in every lane.
 __host__ __device__ constexpr size_t rms_sq_doubles(int n) { return (size_t)n + 8; }
 __device__ __forceinline__ int rms_sq_index(int i, int n) { return (i & 3) * (n / 4 + 2) + (i >> 2); }
 
+// Sixteen steps of the lane's chain from one read (lane i of the row holds
+// step i). The leading s_nop keeps the DPP source clear of a VALU write in
+// the two instructions before it, the trailing one keeps acc clear of a
+// read right after.
+__device__ __forceinline__ double rms_row_steps(double acc, double sq, double one) {
+    __asm__(
+        "s_nop 1\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %0, %1, %2 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "+v"(acc)
+        : "v"(sq), "v"(one));
+    return acc;
+}
+
 template <int N>
 __device__ __forceinline__ double rms_chain(const double *sq, int n, int lane) {
-    constexpr int B = 4;                       // 16-byte reads per batch
+    constexpr int AHEAD = 4;                   // reads in flight
     const int len = N ? N : n;
-    const double2 *src = reinterpret_cast<const double2 *>(sq + lane * (len / 4 + 2));
-    const int pairs = len / 8;                 // a multiple of 2B: n % 128 == 0
+    const int groups = len / 64;               // sixteen steps each
+    const double *src = sq + (lane >> 4) * (len / 4 + 2) + (lane & 15);
+    const double one = 1.0;
     double acc = 0.0;
-    double2 a[B], b[B];
+    double buf[AHEAD];
 #pragma unroll
-    for (int t = 0; t < B; ++t) a[t] = src[t];
-    for (int p = 0; p < pairs; p += 2 * B) {
+    for (int t = 0; t < AHEAD; ++t) buf[t] = t < groups ? src[16 * t] : 0.0;
+    auto round = [&](int g) {
 #pragma unroll
-        for (int t = 0; t < B; ++t) b[t] = src[p + B + t];
-#pragma unroll
-        for (int t = 0; t < B; ++t) {
-            acc = acc + a[t].x;
-            acc = acc + a[t].y;
+        for (int t = 0; t < AHEAD; ++t) {
+            if (g + t < groups) {
+                const double v = buf[t];
+                if (g + t + AHEAD < groups) buf[t] = src[16 * (g + t + AHEAD)];
+                acc = rms_row_steps(acc, v, one);
+            }
         }
-        // The last round reads the chain's first squares again (in range, unused).
-        const int q = p + 2 * B < pairs ? p + 2 * B : 0;
+    };
+    if constexpr (N != 0) {
 #pragma unroll
-        for (int t = 0; t < B; ++t) a[t] = src[q + t];
-#pragma unroll
-        for (int t = 0; t < B; ++t) {
-            acc = acc + b[t].x;
-            acc = acc + b[t].y;
-        }
+        for (int g = 0; g < N / 64; g += AHEAD) round(g);
+    } else {
+        for (int g = 0; g < groups; g += AHEAD) round(g);
     }
     return acc;
 }
 
 __device__ __forceinline__ float rms_scale_wave(const double *sq, int n, float eps) {
     const int lane = threadIdx.x & 63;
-    double acc = 0.0;
     // The hidden size of the decode shapes with its trip count known (the
-    // compiler then unrolls the chain and issues its reads ahead of the
-    // adds); any other n in a loop.
-    if (lane < 4) acc = n == 2048 ? rms_chain<2048>(sq, n, lane) : rms_chain<0>(sq, n, lane);
-    const double l1 = __shfl(acc, 1), l2 = __shfl(acc, 2), l3 = __shfl(acc, 3), l0 = __shfl(acc, 0);
+    // compiler then unrolls the chain); any other n in a loop.
+    const double acc = n == 2048 ? rms_chain<2048>(sq, n, lane) : rms_chain<0>(sq, n, lane);
+    const double l0 = __shfl(acc, 0), l1 = __shfl(acc, 16), l2 = __shfl(acc, 32), l3 = __shfl(acc, 48);
     const double ss = (l0 + l2) + (l1 + l3);
     return 1.0f / sqrtf((float)(ss / (double)n) + eps);
 }
