@@ -147,8 +147,9 @@ int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, 
  * computed once per output instead of by every workgroup of down.
  * 2048 <= k <= 8192, n a multiple of r = 64 / (k / 256) rows (whole tiles of
  * r rows in each half), and the n / r tiles of each half a multiple of 2 when
- * k > 2048 and of 4 when k > 4096 (a workgroup holds one thread per
- * activation block and divides them); other shapes return W4A8_ERR_SHAPE. */
+ * k > 4096 (a workgroup pairs V gate tiles with their V up tiles, one per
+ * wave, V dividing the half, and holds one thread per activation block);
+ * other shapes return W4A8_ERR_SHAPE. */
 int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, float eps, float *act, int rows, int k,
                            void *stream);
 

@@ -191,9 +191,10 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
         const int C = s.k / 256, rpw = 64 / C, tiles = (s.rows + rpw - 1) / rpw;
         M1Shape sh = gemv_m1_shape(tiles, s.k, xf, s.kind == W4A8_PLAN_ARGMAX, cus);
         if (s.kind == W4A8_PLAN_GATE_UP_SILU) {
-            // gate|up's shape (launch_gemv_gate_up_silu): tiles / 2 waves, rows r and r + rows / 2 per wave.
+            // gate|up's shape (launch_gemv_gate_up_silu): workgroups of waves / 2
+            // gate waves and their up partners, one tile each.
             const int waves = gate_up_silu_waves(s.rows, s.k);
-            sh.grid = tiles / 2 / waves;
+            sh.grid = tiles / 2 / (waves / 2);
             sh.threads = 64 * waves;
             sh.lds = (size_t)waves * TILE_BYTES + x_lds_bytes(s.k / QK) + (rms ? rms_sq_doubles(s.k) * 8 + 16 : 0);
         }

@@ -187,10 +187,11 @@ hipError_t launch_batch_pass(const BatchParams &B, int max_k, hipStream_t stream
     return hipGetLastError();
 }
 
-// Waves per workgroup of the gate|up + silu launch: the grid has exactly
-// tiles / 2 waves (a wave's second tile is its first + tiles / 2), so the
-// workgroup size must divide tiles / 2 and hold one thread per activation
-// block; 0 when no size does (or the shape is outside 2048 <= k <= 8192,
+// Waves per workgroup of the gate|up + silu launch: V gate waves and their V
+// up partners, one tile each, so V must divide tiles / 2 (the grid is
+// tiles / 2 / V workgroups) and the 2V waves must hold one thread per
+// activation block. V = 4 where it fits (eight waves, as the plain gate|up
+// GEMV runs); 0 when no V does (or the shape is outside 2048 <= k <= 8192,
 // whole tiles in each half).
 int gate_up_silu_waves(int rows, int k) {
     if (k % 256 || k < 2048 || k > 8192 || rows < 2 || rows % 2) return 0;
@@ -199,8 +200,8 @@ int gate_up_silu_waves(int rows, int k) {
     const int half = rows / 2 / rpw;
     const int nb = k / QK;
     const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;
-    for (int wv = 4; wv >= min_waves && wv >= 1; wv >>= 1)
-        if (half % wv == 0) return wv;
+    for (int v = 4; 2 * v >= min_waves && v >= 1; v >>= 1)
+        if (half % v == 0) return 2 * v;
     return 0;
 }
 
@@ -214,7 +215,7 @@ hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf
     P.eps = aux.eps;
     const int half = P.tiles / 2;
     const int nb = k / QK;
-    const int grid = half / waves;
+    const int grid = half / (waves / 2);
     const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? rms_sq_doubles(k) * 8 + 16 : 0);
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
     if (xf == X_RMS) return launch_pass<X_RMS, true, true, false, true>(P, grid, 64 * waves, lds, stream);

@@ -242,11 +242,14 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
     }
 }
 
-// PAIR: the gate|up GEMV with silu(gate) * up as its epilogue. A wave's two
-// tiles are t and t + tiles / 2 (the grid has exactly tiles / 2 waves):
-// rows r and r + rows / 2, gate and up of the same output. The gate's y stays
-// in the lane's register until the up tile's y is ready, and only
-// act[r] = silu_mul(gate, up) is stored, to y[0 .. rows / 2).
+// PAIR: the gate|up GEMV with silu(gate) * up as its epilogue. Gate tile t
+// (rows of y[0 .. rows / 2)) and up tile t + tiles / 2 (the up rows of the
+// same outputs) go to partner waves of one workgroup: its first waves / 2
+// waves take gate tiles V b .. V b + V - 1 (V = waves / 2, b the workgroup),
+// the others the matching up tiles, one tile each (the grid is exactly
+// tiles / 2 / V workgroups). A gate wave leaves its rows' y in its slab, and
+// after a workgroup barrier its partner stores act[r] = silu_mul(gate, up)
+// to y[0 .. rows / 2).
 // COH (the chain plan's dispatches, which carry no cache fences between
 // them): bit 0, x is an earlier step's output, read from the device's
 // coherence point (past the L2 of this XCD); bit 1, y is a later step's x,
@@ -276,8 +279,10 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     const int trows = paired ? 2 * P.prw : rpw;
 
     constexpr int DEPTH = depth_of<PLAIN>();
-    int tile = block * waves + wave;
-    const int tstride = nblocks * waves;
+    const int pv = waves >> 1;            // PAIR: gate waves per workgroup
+    const bool up_wave = PAIR && wave >= pv;
+    int tile = PAIR ? (up_wave ? (P.tiles >> 1) + block * pv + wave - pv : block * pv + wave) : block * waves + wave;
+    const int tstride = PAIR ? P.tiles : nblocks * waves;
     const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
 
     // 1. The activation. Its loads go out before any weight tile's; the
@@ -349,7 +354,6 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     unsigned long long best = 0;          // argmax epilogue: this lane's best key
     const __amdgpu_buffer_rsrc_t y_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * (PAIR ? P.rows / 2 : P.rows), BUFFER_DWORD3);
-    float held = 0.0f;                    // PAIR: this lane's gate value
     // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
     // slab -> ordered lane sums -> tree -> y; with REFILL the buffer then
     // receives the tile DEPTH strides ahead while the terms are computed.
@@ -386,14 +390,20 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         };
         auto row_of = [&](int r) { return PLAIN ? (r < rpw && tile * rpw + r < P.rows ? tile * rpw + r : -1) : board_row(P, tile, r); };
         if constexpr (PAIR) {
-            // Both halves issue one store; the gate's goes out of range.
+            // The gate wave's y goes to the first floats of its slab (its
+            // ordered sums, read above by this same wave, are done with it);
+            // the up wave reads its partner's after the barrier. Every wave
+            // of the workgroup has exactly one tile, so each reaches it once.
             const float yv = tree8_dpp(lane_sum(acc_r));
-            const int row = tile * rpw + acc_r;
-            const bool up = tile >= (P.tiles >> 1);
-            const bool mine = acc_r < rpw && acc_a == 0 && row < P.rows;
-            held = up ? held : yv;
-            const float act = silu_mul(held, yv);
-            store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, up && mine ? 4 * (row - (P.rows >> 1)) : OUT_OF_RANGE, act);
+            const bool mine = acc_r < rpw && acc_a == 0;
+            if (!up_wave && mine) s_t[acc_r] = yv;
+            __syncthreads();
+            if (up_wave) {
+                const float gate = reinterpret_cast<const float *>(lds + (size_t)(wave - pv) * TILE_BYTES)[acc_r < rpw ? acc_r : 0];
+                const int row = (tile - (P.tiles >> 1)) * rpw + acc_r;
+                const float act = silu_mul(gate, yv);
+                store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, mine && row < (P.rows >> 1) ? 4 * row : OUT_OF_RANGE, act);
+            }
         } else if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
             const int row = row_of(acc_r);

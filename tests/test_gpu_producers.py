@@ -109,7 +109,8 @@ def test_lm_head_step(gpu):
 
 
 @pytest.mark.parametrize("rows,k,rms", [(16384, 2048, True), (16384, 2048, False), (256, 8192, True),
-                                        (4096, 4096, False), (16, 2048, True)])
+                                        (4096, 4096, False), (16, 2048, True), (8, 4096, True), (48, 2048, False),
+                                        (40, 8192, True)])
 def test_gemv_gate_up_silu(gpu, rows, k, rms):
     """gate|up with silu(gate) * up as the epilogue: act = silu_mul(y[:n], y[n:])
     of the plain (or rmsnorm-fed) GEMV, byte for byte."""
@@ -137,8 +138,8 @@ def test_gemv_gate_up_silu_rejects(gpu):
     assert call(63, 2048) == -2        # odd rows
     assert call(12, 2048) == -2        # n = 6 is not a multiple of 8 rows per tile
     assert call(64, 1024) == -2        # k below 2048
-    assert call(4, 8192) == -2         # one tile per half at k = 8192: not a multiple of 4
-    assert call(8, 4096) == -2         # one tile per half at k = 4096: not a multiple of 2
+    assert call(4, 8192) == -2         # one tile per half at k = 8192: not a multiple of 2
     assert call(12, 8192) == -2        # three tiles per half at k = 8192
+    assert call(4, 4096) == -2         # two rows per half at k = 4096: not a whole tile of 4
     assert call(64, 2048) == 0
     torch.cuda.synchronize()
