@@ -41,8 +41,9 @@ Prints one JSON line. Besides the chain (value), it reports:
   gemm         the M > 1 sweep (M = 1 .. 64) at gate|up and down
   lm_head_argmax  the LM head with its greedy pick fused, and the sampler's
                top-40 candidates of the same logits (w4a8_topk)
-  producers    rmsnorm / silu*up fused into the GEMV's staging against the
-               standalone producer then the GEMV
+  producers    rmsnorm / silu*up fused into the GEMV (staging or epilogue)
+               against the standalone producer then the GEMV, and the same
+               GEMV with no producer
   chain_fused_producers  the chain with those producers and the argmax
   prefill      24- and 64-token prompts through the 65 matrices (M > 1 GEMM)
   caller       the reference's decode-side caller (engine_t of
@@ -269,15 +270,17 @@ def time_lm_argmax(torch, kv, cf, stream):
 
 
 def time_producers(torch, kv, cf, stream):
-    """us per GEMV with its producer fused into the activation staging (rmsnorm
-    before q|k|v, gate|up and the LM head; silu(gate) * up before down), next to
-    the same work as two launches (standalone producer + engine-layout GEMV)
-    and the plain fp32 GEMV; weights rotated as for the per-shape GEMVs."""
+    """us per GEMV with its producer fused (rmsnorm in the staging before q|k|v,
+    gate|up and the LM head; silu(gate) * up in down's staging, or as gate|up's
+    epilogue), next to the same work as two launches (standalone producer +
+    engine-layout GEMV) where one gives the same output, and the same GEMV on
+    an fp32 x with no producer; weights rotated as for the per-shape GEMVs."""
     L = kv.lib()
     out = {}
     ws = kv.argmax_workspace()
     best = torch.empty(1, dtype=torch.int32, device="cuda")
     cases = (("qkv_rmsnorm", cf.LAYER_SHAPES[0], "rms"), ("gate_up_rmsnorm", cf.LAYER_SHAPES[2], "rms"),
+             ("gate_up_rmsnorm_silu_epilogue", cf.LAYER_SHAPES[2], "pair"),
              ("down_silu_mul", cf.LAYER_SHAPES[3], "silu"), ("lm_head_rmsnorm_argmax", cf.LM_HEAD, "rms_argmax"))
     for name, m, kind in cases:
         base = device_weights(torch, kv, m.rows, m.k, 9)
@@ -292,6 +295,9 @@ def time_producers(torch, kv, cf, stream):
         launches = max(copies, 30)
 
         def fused(w, s):
+            if kind == "pair":
+                return L.w4a8_gemv_gate_up_silu(w.data_ptr(), xin.data_ptr(), norm.data_ptr(), 1e-5, y.data_ptr(),
+                                                m.rows, m.k, s)
             if kind == "silu":
                 return L.w4a8_gemv_silu_mul(w.data_ptr(), xin.data_ptr(), y.data_ptr(), m.rows, m.k, s)
             if kind == "rms":
@@ -305,8 +311,15 @@ def time_producers(torch, kv, cf, stream):
                   L.w4a8_rmsnorm_q8_0(xin.data_ptr(), norm.data_ptr(), 1e-5, xe.data_ptr(), m.k, 1, s))
             return st or L.w4a8_gemv(w.data_ptr(), xe.data_ptr(), y.data_ptr(), m.rows, m.k, s)
 
+        def plain(w, s):
+            # The same GEMV on an fp32 x with no producer (fused quantize only).
+            return L.w4a8_gemv_f32(w.data_ptr(), xin.data_ptr(), y.data_ptr(), m.rows, m.k, s)
+
         r = {"shape": f"{m.rows}x{m.k}"}
-        for label, fn in (("fused_us", fused), ("two_launches_us", split)):
+        # gate|up with the silu epilogue has no two-launch form of the same output.
+        forms = (("fused_us", fused), ("plain_f32_us", plain)) if kind == "pair" else \
+            (("fused_us", fused), ("two_launches_us", split), ("plain_f32_us", plain))
+        for label, fn in forms:
             calls = [(lambda w: (lambda st: kv.check(name, fn(w, st))))(mats[i % copies]) for i in range(launches)]
             gr = graph_of(torch, stream, calls)
             ms, _ = time_replays(torch, stream, gr, 10, 2)
@@ -318,7 +331,7 @@ def time_producers(torch, kv, cf, stream):
     return out
 
 
-def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu_epilogue=True):
+def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu_epilogue=True, plan=True):
     """The decode step with its producers fused and its one in-step data
     dependency kept: per layer q|k|v = W rmsnorm(x), o = W x, gate|up =
     W rmsnorm(x), down = W (silu(gate) * up) of gate|up's own output; the LM
@@ -371,7 +384,7 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu
            "silu": "gate|up epilogue" if silu_epilogue else "down's staging",
            "issued_by": "the stream entry points from a HIP graph",
            "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
-    if not silu_epilogue:
+    if not silu_epilogue or not plan:
         return out
     # The same steps as a chain plan (w4a8_chain_plan_create_steps), then its
     # outputs and pick against the graph's, byte for byte.
@@ -769,13 +782,15 @@ def main() -> int:
         print(json.dumps(out), flush=True)
         return 0 if out["verified"] else 1
 
-    fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup)
+    fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup,
+                                   plan=not args.no_plan)
     staged = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, silu_epilogue=False)
     fused_chain["silu_in_down_staging_us_per_step"] = staged["us_per_step"]
     log(f"fused chain: {fused_chain['us_per_step']} us/step, {fused_chain['tokens_per_s']} tokens/s "
         f"(rmsnorm fused, silu in gate|up's epilogue, LM head with argmax); {staged['us_per_step']} us/step "
-        f"with silu in down's staging; as a chain plan {fused_chain['plan']['us_per_step']} us/step, "
-        f"verified {fused_chain['plan']['verified']}")
+        f"with silu in down's staging" + ("" if "plan" not in fused_chain else
+                                          f"; as a chain plan {fused_chain['plan']['us_per_step']} us/step, "
+                                          f"verified {fused_chain['plan']['verified']}"))
 
     gemv, gemm = {}, []
     shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES
@@ -796,7 +811,8 @@ def main() -> int:
             torch.cuda.empty_cache()
     producers = {} if args.no_gemv else time_producers(torch, kv, cf, stream)
     for name, r in producers.items():
-        log(f"producer {name} {r['shape']}: fused {r['fused_us']} us, two launches {r['two_launches_us']} us")
+        log(f"producer {name} {r['shape']}: fused {r['fused_us']} us, two launches {r.get('two_launches_us')} us, "
+            f"no producer {r['plain_f32_us']} us")
     lm_argmax = time_lm_argmax(torch, kv, cf, stream)
     log(f"gemv lm_head + argmax: {lm_argmax['us']} us, {lm_argmax['gbps']} GB/s")
     log(f"top-{lm_argmax['topk']['k']} candidates of the logits: {lm_argmax['topk']['us']} us "
@@ -818,14 +834,14 @@ def main() -> int:
         log("CPU baseline (bounded sample)")
         cpu = cpu_baseline(chain, mats, xs)
     verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and graph["verified"] and
-                fused_chain["plan"]["verified"] and
+                fused_chain.get("plan", {}).get("verified", True) and
                 (one_launch is None or one_launch["verified"]) and
                 all(r["verified"] for r in gemm) and prefill[0]["verified"] is True)
 
     out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph)
     out["verified"] = verified
     out["verification"] = {"chain": chain_check, "chain_graph": graph_check, "batch": batch_check,
-                           "fused_chain_plan": fused_chain["plan"]["verified"],
+                           "fused_chain_plan": fused_chain.get("plan", {}).get("verified"),
                            "one_launch": one_launch["verified"] if one_launch else None,
                            "gemm": {f"{r['name']} M={r['m']}": r["verified"] for r in gemm},
                            "prefill24": prefill[0]["verification"],

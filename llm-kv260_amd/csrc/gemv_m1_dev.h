@@ -470,14 +470,23 @@ __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(const uint8_t *w0,
                                                               int rpw, int tiles, int nblocks, int nthreads,
                                                               GemvParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    P.seg[0] = w0;
-    P.x = x;
-    P.rows = rows;
-    P.k = k;
-    P.C = C;
-    P.rpw = rpw;
-    P.tiles = tiles;
-    gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>(P, blockIdx.x, nblocks, nthreads, lds);
+    if constexpr (PLAIN) {
+        P.seg[0] = w0;
+        P.x = x;
+        P.rows = rows;
+        P.k = k;
+        P.C = C;
+        P.rpw = rpw;
+        P.tiles = tiles;
+        gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>(P, blockIdx.x, nblocks, nthreads, lds);
+    } else {
+        // The board layouts index P.seg at run time: P stays as the host wrote
+        // it (the leading scalars repeat its fields) and is read from the
+        // argument block. Writing to it would make it a local copy, which the
+        // run-time index puts in scratch memory (the gemv2 LM head then took
+        // 60 us instead of 35).
+        gemv_m1_body<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>(P, blockIdx.x, nblocks, nthreads, lds);
+    }
 }
 
 __host__ __device__ inline void derive_plain(GemvParams &P, const uint8_t *w, const void *x, float *y, int rows, int k) {
