@@ -3,8 +3,8 @@ library's own queue, no cache fences between steps): each step byte for byte
 against the oracle and against w4a8_chain_gemv, over several passes and
 launches; a step-to-step data dependency inside a pass and one that runs from
 the last step of a pass into the first step of the next (the coherent-read
-and write-through variants); several launches before one wait; plans made
-and destroyed in turn.
+and write-through variants), readers of memory an earlier step already
+cached; several launches before one wait; plans made and destroyed in turn.
 
 Every output buffer is poisoned with 0xAA first.
 """
@@ -149,6 +149,43 @@ def test_plan_dependency_across_passes(gpu):
     wants = _dependent_oracle(blocks, shapes, x, 2)
     for i, (y, want) in enumerate(zip(ys, wants)):
         assert_bytes_equal(host(y), want, f"after 3 + 2 passes, step {i}")
+    plan.close()
+
+
+def test_plan_reader_paths(gpu):
+    """Steps reading other steps' outputs where an earlier step of the pass
+    has already brought that memory into an L2: a second reader of one
+    output, and an output sharing an L2 line with an earlier step's input (one
+    arena, the two 16 bytes apart across a line), besides plain readers."""
+    import torch
+    k = 2048
+    blocks = [C.quantize_q4_0(O.normal_f32((k, k), 120 + i, 0.02)) for i in range(5)]
+    mats = [dev(b) for b in blocks]
+    xa = O.normal_f32((1, k), 119)[0]
+    arena = torch.full((2 * k + 1024,), float("nan"), dtype=torch.float32, device="cuda")
+    x_in = arena[16:16 + k]                          # bytes 64 .. 8256
+    y_p = arena[16 + k + 4:16 + 2 * k + 4]           # from byte 8272: same 256-byte line as x_in's end
+    x_in.copy_(dev(xa))
+    y0, y2, y3, y4 = (poisoned_f32(k) for _ in range(4))
+    # step: (x, y); 1 reads y0, 3 reads y0 again, 2 reads y_p (its first line
+    # shared with step 0's input), 4 reads y2
+    io = [(x_in, y0), (y0, y_p), (y_p, y2), (y0, y3), (y2, y4)]
+    steps = (Step * 5)(*[Step(mats[i].data_ptr(), x.data_ptr(), y.data_ptr(), k, k) for i, (x, y) in enumerate(io)])
+    def q(v):
+        return C.quantize_q8_0(np.asarray(v, dtype=np.float32))
+    w0 = C.gemv_q4_0(blocks[0], k, *q(xa))
+    w1 = C.gemv_q4_0(blocks[1], k, *q(w0))
+    w2 = C.gemv_q4_0(blocks[2], k, *q(w1))
+    w3 = C.gemv_q4_0(blocks[3], k, *q(w0))
+    w4 = C.gemv_q4_0(blocks[4], k, *q(w2))
+    plan = Plan(gpu, steps, 5)
+    for passes in (1, 3):
+        for y in (y0, y_p, y2, y3, y4):
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        plan.run(passes)
+        for name, y, want in (("y0", y0, w0), ("y_p", y_p, w1), ("y2", y2, w2), ("y3", y3, w3), ("y4", y4, w4)):
+            assert_bytes_equal(host(y), want, f"{passes} passes, {name}")
     plan.close()
 
 
