@@ -331,16 +331,19 @@ def time_producers(torch, kv, cf, stream):
     return out
 
 
-def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu_epilogue=True, plan=True):
+def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, act="q8", plan=True):
     """The decode step with its producers fused and its one in-step data
     dependency kept: per layer q|k|v = W rmsnorm(x), o = W x, gate|up =
     W rmsnorm(x), down = W (silu(gate) * up) of gate|up's own output; the LM
     head = W rmsnorm(x) with its greedy pick. The rmsnorm inputs (the residual
     stream) and o's input (the attention output) are seeded vectors: attention
-    and the residual adds are not part of the engine. silu_epilogue: gate|up
-    computes silu(gate) * up as its epilogue (w4a8_gemv_gate_up_silu) and down
-    quantizes that; otherwise down computes silu in its own staging
-    (w4a8_gemv_silu_mul)."""
+    and the residual adds are not part of the engine. act: "q8", gate|up
+    computes silu(gate) * up and quantizes it in its epilogue
+    (w4a8_gemv_gate_up_silu_q8_0) and down reads that engine-layout x
+    (w4a8_gemv); "f32", gate|up stores the fp32 act (w4a8_gemv_gate_up_silu)
+    and down quantizes it (w4a8_gemv_f32); "down", down computes silu in its
+    own staging (w4a8_gemv_silu_mul). plan: also as a chain plan, every output
+    checked against the graph's."""
     L = kv.lib()
     g = torch.Generator(device="cuda")
     g.manual_seed(6)
@@ -350,17 +353,26 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu
     norm = torch.randn(k, generator=g, device="cuda")
     ws = kv.argmax_workspace()
     best = torch.empty(1, dtype=torch.int32, device="cuda")
+    role_of = lambda i: "lm" if i == len(chain) - 1 else ("qkv", "o", "gate_up", "down")[i % 4]
+    # q8: each layer's act in the engine layout, written by gate|up, read by down
+    acts = {i: torch.empty(kv.engine_x_bytes(m.rows // 2), dtype=torch.uint8, device="cuda")
+            for i, m in enumerate(chain) if act == "q8" and role_of(i) == "gate_up"}
     calls = []
     for i, m in enumerate(chain):
-        w, y = mats[i], ys[i]
-        role = "lm" if i == len(chain) - 1 else ("qkv", "o", "gate_up", "down")[i % 4]
-        if role == "gate_up" and silu_epilogue:
+        w, y, role = mats[i], ys[i], role_of(i)
+        if role == "gate_up" and act == "q8":
+            calls.append((lambda w, m, e: lambda s: L.w4a8_gemv_gate_up_silu_q8_0(
+                w.data_ptr(), resid.data_ptr(), norm.data_ptr(), 1e-5, e.data_ptr(), m.rows, m.k, s))(w, m, acts[i]))
+        elif role == "down" and act == "q8":
+            calls.append((lambda w, y, m, e: lambda s: L.w4a8_gemv(w.data_ptr(), e.data_ptr(), y.data_ptr(),
+                                                                   m.rows, m.k, s))(w, y, m, acts[i - 1]))
+        elif role == "gate_up" and act == "f32":
             calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_gate_up_silu(
                 w.data_ptr(), resid.data_ptr(), norm.data_ptr(), 1e-5, y.data_ptr(), m.rows, m.k, s))(w, y, m))
-        elif role == "down" and silu_epilogue:
-            act = ys[i - 1]                                  # gate|up's act, its first half
-            calls.append((lambda w, y, m, act: lambda s: L.w4a8_gemv_f32(w.data_ptr(), act.data_ptr(), y.data_ptr(),
-                                                                         m.rows, m.k, s))(w, y, m, act))
+        elif role == "down" and act == "f32":
+            a = ys[i - 1]                                    # gate|up's act, its first half
+            calls.append((lambda w, y, m, a: lambda s: L.w4a8_gemv_f32(w.data_ptr(), a.data_ptr(), y.data_ptr(),
+                                                                       m.rows, m.k, s))(w, y, m, a))
         elif role in ("qkv", "gate_up"):
             calls.append((lambda w, y, m: lambda s: L.w4a8_gemv_rmsnorm(w.data_ptr(), resid.data_ptr(), norm.data_ptr(),
                                                                         1e-5, y.data_ptr(), m.rows, m.k, s))(w, y, m))
@@ -381,24 +393,35 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu
     del gr
     out = {"us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "launches_per_step": len(calls),
            "gbps": round(cf.chain_algorithmic_bytes() / (ms * 1e-3) / 1e9, 1),
-           "silu": "gate|up epilogue" if silu_epilogue else "down's staging",
+           "act": {"q8": "gate|up epilogue quantizes silu(gate) * up; down reads the engine layout",
+                   "f32": "gate|up epilogue stores silu(gate) * up as fp32; down quantizes it",
+                   "down": "down computes silu(gate) * up in its own staging"}[act],
            "issued_by": "the stream entry points from a HIP graph",
-           "dependency": "matrix j+1 after matrix j; down reads gate|up's output through silu(gate) * up"}
-    if not silu_epilogue or not plan:
+           "dependency": "matrix j+1 after matrix j; down reads gate|up's output"}
+    if act == "down" or not plan:
         return out
     # The same steps as a chain plan (w4a8_chain_plan_create_steps), then its
     # outputs and pick against the graph's, byte for byte.
     torch.cuda.synchronize()
-    ref = [y.clone() for y in ys] + [best.clone()]
+    # What each step writes: gate|up's act (its first rows / 2 floats, or the
+    # engine buffer), every other y whole.
+    written = []
+    for i, (m, y) in enumerate(zip(chain, ys)):
+        if role_of(i) == "gate_up":
+            written.append(acts[i] if act == "q8" else y[:m.rows // 2])
+        else:
+            written.append(y)
+    ref = [t.clone() for t in written] + [best.clone()]
     S, plan_steps = kv.PlanStep, []
     for i, m in enumerate(chain):
-        w, y = mats[i], ys[i]
-        role = "lm" if i == len(chain) - 1 else ("qkv", "o", "gate_up", "down")[i % 4]
+        w, y, role = mats[i], ys[i], role_of(i)
         if role == "gate_up":
-            plan_steps.append(S(kv.PLAN_GATE_UP_SILU, w.data_ptr(), resid.data_ptr(), y.data_ptr(), m.rows, m.k,
-                                norm.data_ptr(), 1e-5))
+            kind, dst = (kv.PLAN_GATE_UP_SILU_Q8, acts[i]) if act == "q8" else (kv.PLAN_GATE_UP_SILU, y)
+            plan_steps.append(S(kind, w.data_ptr(), resid.data_ptr(), dst.data_ptr(), m.rows, m.k, norm.data_ptr(),
+                                1e-5))
         elif role == "down":
-            plan_steps.append(S(kv.PLAN_GEMV, w.data_ptr(), ys[i - 1].data_ptr(), y.data_ptr(), m.rows, m.k, None, 0.0))
+            kind, src = (kv.PLAN_GEMV_ENGINE, acts[i - 1]) if act == "q8" else (kv.PLAN_GEMV, ys[i - 1])
+            plan_steps.append(S(kind, w.data_ptr(), src.data_ptr(), y.data_ptr(), m.rows, m.k, None, 0.0))
         elif role == "qkv":
             plan_steps.append(S(kv.PLAN_GEMV, w.data_ptr(), resid.data_ptr(), y.data_ptr(), m.rows, m.k,
                                 norm.data_ptr(), 1e-5))
@@ -415,6 +438,8 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu
         kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, max(warmup, 1)))
         kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
         poison(ys)
+        for e in acts.values():
+            e.fill_(0xAA)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, steps))
@@ -423,11 +448,7 @@ def time_fused_chain(torch, kv, cf, chain, mats, ys, stream, steps, warmup, silu
         torch.cuda.synchronize()
     finally:
         kv.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
-    # gate|up with the silu epilogue writes rows/2 values (silu(gate) * up);
-    # the rest of its output buffer is not an output.
-    written = [y[:m.rows // 2] if i % 4 == 2 and i != len(chain) - 1 else y for i, (m, y) in enumerate(zip(chain, ys))]
-    same = all(torch.equal(a.view(torch.int32), b[:a.numel()].view(torch.int32))
-               for a, b in zip(written + [best], ref))
+    same = all(torch.equal(a.view(torch.uint8), b.view(torch.uint8)) for a, b in zip(written + [best], ref))
     out["plan"] = {"us_per_step": round(dt * 1e6 / steps, 2), "tokens_per_s": round(steps / dt, 1),
                    "issued_by": "w4a8_chain_plan_create_steps / _launch / _wait",
                    "verified": same, "verification": "every output and the picked row equal the graph's"}
@@ -782,15 +803,21 @@ def main() -> int:
         print(json.dumps(out), flush=True)
         return 0 if out["verified"] else 1
 
-    fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup,
+    fused_chain = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, act="q8",
                                    plan=not args.no_plan)
-    staged = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, silu_epilogue=False)
+    fused_f32 = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, act="f32",
+                                 plan=not args.no_plan)
+    staged = time_fused_chain(torch, kv, cf, chain, mats, ys, stream, args.steps, args.warmup, act="down")
+    fused_chain["fp32_act"] = {"us_per_step": fused_f32["us_per_step"], "act": fused_f32["act"]}
+    if "plan" in fused_f32:
+        fused_chain["fp32_act"]["plan"] = fused_f32["plan"]
     fused_chain["silu_in_down_staging_us_per_step"] = staged["us_per_step"]
-    log(f"fused chain: {fused_chain['us_per_step']} us/step, {fused_chain['tokens_per_s']} tokens/s "
-        f"(rmsnorm fused, silu in gate|up's epilogue, LM head with argmax); {staged['us_per_step']} us/step "
-        f"with silu in down's staging" + ("" if "plan" not in fused_chain else
-                                          f"; as a chain plan {fused_chain['plan']['us_per_step']} us/step, "
-                                          f"verified {fused_chain['plan']['verified']}"))
+    plan_txt = lambda r: "" if "plan" not in r else (f", as a chain plan {r['plan']['us_per_step']} us/step "
+                                                     f"(verified {r['plan']['verified']})")
+    log(f"fused chain (rmsnorm fused, silu in gate|up's epilogue, LM head with argmax): act quantized in the "
+        f"epilogue {fused_chain['us_per_step']} us/step{plan_txt(fused_chain)}; fp32 act "
+        f"{fused_f32['us_per_step']} us/step{plan_txt(fused_f32)}; silu in down's staging "
+        f"{staged['us_per_step']} us/step")
 
     gemv, gemm = {}, []
     shapes = (cf.LM_HEAD,) if args.no_gemv else (cf.LM_HEAD, cf.O_PROJ) + cf.LAYER_SHAPES
@@ -835,6 +862,7 @@ def main() -> int:
         cpu = cpu_baseline(chain, mats, xs)
     verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and graph["verified"] and
                 fused_chain.get("plan", {}).get("verified", True) and
+                fused_chain["fp32_act"].get("plan", {}).get("verified", True) and
                 (one_launch is None or one_launch["verified"]) and
                 all(r["verified"] for r in gemm) and prefill[0]["verified"] is True)
 
@@ -842,6 +870,7 @@ def main() -> int:
     out["verified"] = verified
     out["verification"] = {"chain": chain_check, "chain_graph": graph_check, "batch": batch_check,
                            "fused_chain_plan": fused_chain.get("plan", {}).get("verified"),
+                           "fused_chain_fp32_act_plan": fused_chain["fp32_act"].get("plan", {}).get("verified"),
                            "one_launch": one_launch["verified"] if one_launch else None,
                            "gemm": {f"{r['name']} M={r['m']}": r["verified"] for r in gemm},
                            "prefill24": prefill[0]["verification"],

@@ -153,6 +153,18 @@ int w4a8_gemv_silu_mul(const void *w, const float *gate_up, float *y, int rows, 
 int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, float eps, float *act, int rows, int k,
                            void *stream);
 
+/* The same with act quantized to Q8_0 in the epilogue: act_engine receives
+ * the engine layout of the n values (int8[n] | float32[n / 32], 16-byte
+ * aligned; n + n / 8 bytes), byte-identical to w4a8_gemv_gate_up_silu then
+ * w4a8_quantize_q8_0 -- the input of w4a8_gemv for down, as the
+ * reference's caller quantizes x before each engine call
+ * (tp_llama.cpp:330-352). Down then reads n + n / 8 bytes instead of 4n.
+ * k = 2048 only, and the n / 8 tiles of each half a multiple of 4 (a
+ * workgroup's 32 outputs are one Q8_0 block); other shapes return
+ * W4A8_ERR_SHAPE. No counterpart in the reference (its host quantizes). */
+int w4a8_gemv_gate_up_silu_q8_0(const void *w, const float *x, const float *norm_w, float eps, void *act_engine,
+                                int rows, int k, void *stream);
+
 /* The same producers on their own, m rows, quantized to the engine layout
  * (row stride w4a8_engine_x_bytes(k)): the input of w4a8_gemv / w4a8_gemm. */
 int w4a8_rmsnorm_q8_0(const float *x, const float *norm_w, float eps, void *out_engine, int k, int m, void *stream);
@@ -269,7 +281,13 @@ int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan 
  *                             when norm_w is set: *argmax = the row picked,
  *                             through `workspace` (w4a8_argmax_workspace_bytes(),
  *                             zero before the first launch; the step leaves
- *                             it zero).
+ *                             it zero);
+ *   W4A8_PLAN_GATE_UP_SILU_Q8 w4a8_gemv_gate_up_silu_q8_0: y = the engine
+ *                             layout of silu(gate) * up, rows / 2 values
+ *                             (k = 2048, its shape rules);
+ *   W4A8_PLAN_GEMV_ENGINE     w4a8_gemv: x in the engine layout
+ *                             (int8[k] | float32[k / 32]), norm_w NULL --
+ *                             down after W4A8_PLAN_GATE_UP_SILU_Q8.
  * Every k in 2048..W4A8_MAX_K; the rest as w4a8_chain_plan_create (which is
  * this with every step a W4A8_PLAN_GEMV without norm_w). A step may read an
  * earlier (or, over passes, a later) step's y; norm_w, argmax and the
@@ -277,11 +295,13 @@ int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan 
 #define W4A8_PLAN_GEMV 0
 #define W4A8_PLAN_GATE_UP_SILU 1
 #define W4A8_PLAN_ARGMAX 2
+#define W4A8_PLAN_GATE_UP_SILU_Q8 3
+#define W4A8_PLAN_GEMV_ENGINE 4
 typedef struct w4a8_plan_step {
     int kind;
     const void *w;          /* Q4_0 rows, 16-byte aligned */
-    const float *x;         /* float32[k], 16-byte aligned */
-    float *y;               /* float32[rows] (gate|up: [rows / 2]) */
+    const void *x;          /* float32[k] (GEMV_ENGINE: the engine layout), 16-byte aligned */
+    void *y;                /* float32[rows] (gate|up: [rows / 2]; _Q8: its engine layout) */
     int rows;
     int k;
     const float *norm_w;    /* float32[k], 16-byte aligned, or NULL */

@@ -106,6 +106,18 @@ int w4a8_gemv_gate_up_silu(const void *w, const float *x, const float *norm_w, f
                                                k, (hipStream_t)stream, aux));
 }
 
+int w4a8_gemv_gate_up_silu_q8_0(const void *w, const float *x, const float *norm_w, float eps, void *act_engine,
+                                int rows, int k, void *stream) {
+    if (int s = check_gemv(w, x, static_cast<const float *>(act_engine), rows, k, 16)) return s;
+    if (!gate_up_silu_q8_fits(rows, k)) return W4A8_ERR_SHAPE;
+    if (!aligned(act_engine, 16) || (norm_w && !aligned(norm_w, 16))) return W4A8_ERR_ALIGN;
+    XAux aux;
+    aux.norm_w = norm_w;
+    aux.eps = eps;
+    return hip_status(launch_gemv_gate_up_silu(static_cast<const uint8_t *>(w), x, norm_w ? X_RMS : X_F32, act_engine,
+                                               rows, k, (hipStream_t)stream, aux, true));
+}
+
 size_t w4a8_topk_workspace_bytes(int n) { return topk_workspace_bytes(n); }
 
 int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *workspace, size_t workspace_bytes,
@@ -231,13 +243,17 @@ int w4a8_chain_plan_create_steps(const w4a8_plan_step *steps, int n, w4a8_chain_
     // The checks of the stream entry point each step stands for.
     for (int i = 0; i < n; ++i) {
         const w4a8_plan_step &s = steps[i];
-        if (int st = check_gemv(s.w, s.x, s.y, s.rows, s.k, 16)) return st;
-        if (s.k < 2048 || s.kind < W4A8_PLAN_GEMV || s.kind > W4A8_PLAN_ARGMAX) return W4A8_ERR_SHAPE;
+        if (int st = check_gemv(s.w, s.x, static_cast<const float *>(s.y), s.rows, s.k, 16)) return st;
+        if (s.k < 2048 || s.kind < W4A8_PLAN_GEMV || s.kind > W4A8_PLAN_GEMV_ENGINE) return W4A8_ERR_SHAPE;
         if (s.norm_w) {
-            if (s.k > RMS_FUSED_MAX_K) return W4A8_ERR_SHAPE;
+            if (s.k > RMS_FUSED_MAX_K || s.kind == W4A8_PLAN_GEMV_ENGINE) return W4A8_ERR_SHAPE;
             if (!aligned(s.norm_w, 16)) return W4A8_ERR_ALIGN;
         }
         if (s.kind == W4A8_PLAN_GATE_UP_SILU && gate_up_silu_waves(s.rows, s.k) == 0) return W4A8_ERR_SHAPE;
+        if (s.kind == W4A8_PLAN_GATE_UP_SILU_Q8) {
+            if (!gate_up_silu_q8_fits(s.rows, s.k)) return W4A8_ERR_SHAPE;
+            if (!aligned(s.y, 16)) return W4A8_ERR_ALIGN;
+        }
         if (s.kind == W4A8_PLAN_ARGMAX) {
             if (!s.argmax || !s.workspace) return W4A8_ERR_NULL;
             if (!aligned(s.argmax, 4) || !aligned(s.workspace, 16)) return W4A8_ERR_ALIGN;

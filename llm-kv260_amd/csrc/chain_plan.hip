@@ -60,12 +60,41 @@ struct PlanArgs {
 static_assert(sizeof(PlanArgs) == 176, "argument block of the plan's kernels");
 constexpr size_t ARG_STRIDE = 256;
 constexpr uint32_t QUEUE_PACKETS = 16384;
-// Kernel variants: (step kind) x (x as is, or rmsnorm first) x (coherence),
-// in chain_plan_kernels.hip, w4a8_plan_<kind>_<format><coherence>.
-constexpr int N_KINDS = 3, N_KERNELS = N_KINDS * 2 * 4;
-constexpr const char *KIND_NAMES[N_KINDS] = {"gemv", "pair", "argmax"};
+// Kernel variants: (kernel kind) x (x format) x (coherence), in
+// chain_plan_kernels.hip, w4a8_plan_<kind>_<format><coherence>. Not every
+// kind has every format (HAS_FORMAT); the slots of the others stay empty.
+constexpr int N_KKINDS = 4, N_FORMATS = 3, N_KERNELS = N_KKINDS * N_FORMATS * 4;
+constexpr int KK_GEMV = 0, KK_PAIR = 1, KK_ARGMAX = 2, KK_PAIR_Q8 = 3;
+constexpr int FMT_F32 = 0, FMT_RMS = 1, FMT_ENG = 2;
+constexpr const char *KIND_NAMES[N_KKINDS] = {"gemv", "pair", "argmax", "pairq"};
+constexpr const char *FORMAT_NAMES[N_FORMATS] = {"f32", "rms", "eng"};
 constexpr const char *COH_NAMES[4] = {"", "_xc", "_yc", "_xyc"};
-constexpr int kernel_index(int kind, bool rms, int coh) { return (kind * 2 + (rms ? 1 : 0)) * 4 + coh; }
+constexpr bool HAS_FORMAT[N_KKINDS][N_FORMATS] = {{true, true, true}, {true, true, false}, {true, true, false},
+                                                  {true, true, false}};
+constexpr int kernel_index(int kk, int fmt, int coh) { return (kk * N_FORMATS + fmt) * 4 + coh; }
+
+// A plan step's kernel kind and x format.
+int kernel_kind(const w4a8_plan_step &s) {
+    switch (s.kind) {
+        case W4A8_PLAN_GATE_UP_SILU: return KK_PAIR;
+        case W4A8_PLAN_ARGMAX: return KK_ARGMAX;
+        case W4A8_PLAN_GATE_UP_SILU_Q8: return KK_PAIR_Q8;
+        default: return KK_GEMV;
+    }
+}
+int x_format(const w4a8_plan_step &s) {
+    if (s.kind == W4A8_PLAN_GEMV_ENGINE) return FMT_ENG;
+    return s.norm_w ? FMT_RMS : FMT_F32;
+}
+// The bytes a step reads as x and writes as y.
+size_t x_bytes(const w4a8_plan_step &s) {
+    return s.kind == W4A8_PLAN_GEMV_ENGINE ? (size_t)s.k + (size_t)s.k / 8 : 4 * (size_t)s.k;
+}
+size_t y_bytes(const w4a8_plan_step &s) {
+    if (s.kind == W4A8_PLAN_GATE_UP_SILU) return 4 * (size_t)(s.rows / 2);
+    if (s.kind == W4A8_PLAN_GATE_UP_SILU_Q8) return (size_t)(s.rows / 2) + (size_t)(s.rows / 16);
+    return 4 * (size_t)s.rows;
+}
 constexpr double QUEUE_SPACE_WAIT_S = 10.0;    // bound on waiting for free packet slots
 
 struct DeviceRuntime {
@@ -134,10 +163,11 @@ int runtime_of(int dev, DeviceRuntime *&out) {
         hsa_executable_freeze(rt.exe, nullptr) != HSA_STATUS_SUCCESS)
         return rt.status;
     for (int v = 0; v < N_KERNELS; ++v) {
+        const int kk = v / (4 * N_FORMATS), fmt = (v / 4) % N_FORMATS;
+        if (!HAS_FORMAT[kk][fmt]) continue;
         hsa_executable_symbol_t sym;
         char name[64];
-        std::snprintf(name, sizeof name, "w4a8_plan_%s_%s%s.kd", KIND_NAMES[v / 8], (v / 4) % 2 ? "rms" : "f32",
-                      COH_NAMES[v % 4]);
+        std::snprintf(name, sizeof name, "w4a8_plan_%s_%s%s.kd", KIND_NAMES[kk], FORMAT_NAMES[fmt], COH_NAMES[v % 4]);
         if (hsa_executable_get_symbol_by_name(rt.exe, name, &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
             hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &rt.kobj[v]) !=
                 HSA_STATUS_SUCCESS ||
@@ -169,15 +199,11 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
     p->device = dev;
     p->n = n;
     p->kind.assign(n, 0);
-    // Which outputs another step reads, in this pass or the next (gate|up's
-    // output is its rows / 2 products).
-    auto y_bytes = [&](const w4a8_plan_step &s) {
-        return 4 * (size_t)(s.kind == W4A8_PLAN_GATE_UP_SILU ? s.rows / 2 : s.rows);
-    };
+    // Which outputs another step reads, in this pass or the next.
     std::vector<int> coh(n, 0);
     for (int j = 0; j < n; ++j)
         for (int i = 0; i < n; ++i)
-            if (overlaps(steps[j].x, 4 * (size_t)steps[j].k, steps[i].y, y_bytes(steps[i]))) {
+            if (overlaps(steps[j].x, x_bytes(steps[j]), steps[i].y, y_bytes(steps[i]))) {
                 coh[j] |= COH_X;
                 coh[i] |= COH_Y;
             }
@@ -186,11 +212,12 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
     for (int j = 0; j < n; ++j) {
         const w4a8_plan_step &s = steps[j];
         const bool rms = s.norm_w != nullptr;
-        const XFormat xf = rms ? X_RMS : X_F32;
-        p->kind[j] = kernel_index(s.kind, rms, coh[j]);
+        const int fmt = x_format(s);
+        const XFormat xf = fmt == FMT_ENG ? X_ENGINE : (rms ? X_RMS : X_F32);
+        p->kind[j] = kernel_index(kernel_kind(s), fmt, coh[j]);
         const int C = s.k / 256, rpw = 64 / C, tiles = (s.rows + rpw - 1) / rpw;
         M1Shape sh = gemv_m1_shape(tiles, s.k, xf, s.kind == W4A8_PLAN_ARGMAX, cus);
-        if (s.kind == W4A8_PLAN_GATE_UP_SILU) {
+        if (s.kind == W4A8_PLAN_GATE_UP_SILU || s.kind == W4A8_PLAN_GATE_UP_SILU_Q8) {
             // gate|up's shape (launch_gemv_gate_up_silu): workgroups of waves / 2
             // gate waves and their up partners, one tile each.
             const int waves = gate_up_silu_waves(s.rows, s.k);
@@ -211,7 +238,7 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
         a.nthreads = sh.threads;
         for (int g = 0; g < 4; ++g) a.P.seg[g] = a.w0;
         a.P.x = s.x;
-        a.P.y = s.y;
+        a.P.y = static_cast<float *>(s.y);
         a.P.seg_rows = s.rows;
         a.P.nseg = 1;
         a.P.k = s.k;

@@ -1,9 +1,10 @@
 // The chain plan's code object (chain_plan.hip dispatches these kernels as
 // raw AQL packets): the M = 1 GEMV with its fp32 activation quantized in its
 // staging (gemv_m1_dev.h, the same body, byte for byte), with or without the
-// rmsnorm before it, as a plain GEMV, as gate|up with silu * up as its
-// epilogue and as the LM head with its greedy pick, each in four coherence
-// variants and under plain C names. A plan's dispatches carry no cache fences
+// rmsnorm before it, or on an engine-layout activation, as a plain GEMV, as
+// gate|up with silu * up as its epilogue (act as fp32 or quantized) and as
+// the LM head with its greedy pick, each in four coherence variants and
+// under plain C names. A plan's dispatches carry no cache fences
 // between them, so a step whose x an earlier step wrote reads it from the
 // device's coherence point (_xc), and a step whose y a later step reads
 // writes it through (_yc); the others use the caches as usual.
@@ -14,7 +15,7 @@
 namespace w4a8 {
 namespace {
 
-template <int XF, bool ARGMAX, bool PAIR, int COH>
+template <int XF, bool ARGMAX, int PAIR, int COH>
 __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int rows, int k, int C, int rpw, int tiles,
                                           int nblocks, int nthreads, GemvParams &P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -50,12 +51,17 @@ __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int 
     W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT##_yc, XF, ARGMAX, PAIR, w4a8::COH_Y)             \
     W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT##_xyc, XF, ARGMAX, PAIR, w4a8::COH_X | w4a8::COH_Y)
 
-// The GEMV (w4a8_gemv_f32, w4a8_gemv_rmsnorm), gate|up with silu * up as its
-// epilogue (w4a8_gemv_gate_up_silu), the LM head with its greedy pick
-// (w4a8_gemv_f32_argmax, w4a8_gemv_rmsnorm_argmax).
-W4A8_PLAN_KIND(gemv, f32, w4a8::X_F32, false, false)
-W4A8_PLAN_KIND(gemv, rms, w4a8::X_RMS, false, false)
-W4A8_PLAN_KIND(pair, f32, w4a8::X_F32, false, true)
-W4A8_PLAN_KIND(pair, rms, w4a8::X_RMS, false, true)
-W4A8_PLAN_KIND(argmax, f32, w4a8::X_F32, true, false)
-W4A8_PLAN_KIND(argmax, rms, w4a8::X_RMS, true, false)
+// The GEMV (w4a8_gemv_f32, w4a8_gemv_rmsnorm, and w4a8_gemv on an
+// engine-layout x), gate|up with silu * up as its epilogue
+// (w4a8_gemv_gate_up_silu, and w4a8_gemv_gate_up_silu_q8_0 quantizing it),
+// the LM head with its greedy pick (w4a8_gemv_f32_argmax,
+// w4a8_gemv_rmsnorm_argmax).
+W4A8_PLAN_KIND(gemv, f32, w4a8::X_F32, false, 0)
+W4A8_PLAN_KIND(gemv, rms, w4a8::X_RMS, false, 0)
+W4A8_PLAN_KIND(gemv, eng, w4a8::X_ENGINE, false, 0)
+W4A8_PLAN_KIND(pair, f32, w4a8::X_F32, false, w4a8::PAIR_F32)
+W4A8_PLAN_KIND(pair, rms, w4a8::X_RMS, false, w4a8::PAIR_F32)
+W4A8_PLAN_KIND(pairq, f32, w4a8::X_F32, false, w4a8::PAIR_Q8)
+W4A8_PLAN_KIND(pairq, rms, w4a8::X_RMS, false, w4a8::PAIR_Q8)
+W4A8_PLAN_KIND(argmax, f32, w4a8::X_F32, true, 0)
+W4A8_PLAN_KIND(argmax, rms, w4a8::X_RMS, true, 0)

@@ -13,7 +13,7 @@ namespace w4a8 {
 
 namespace {
 
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX, bool PAIR = false>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX, int PAIR = 0>
 hipError_t launch_pass(const GemvParams &P, int grid, int threads, size_t lds, hipStream_t stream) {
     const hipError_t e =
         allow_dynamic_lds(reinterpret_cast<const void *>(&gemv_m1_kernel<XF, PLAIN, ONE_PASS, ARGMAX, PAIR>), LDS_BUDGET);
@@ -205,12 +205,15 @@ int gate_up_silu_waves(int rows, int k) {
     return 0;
 }
 
-hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, float *act, int rows, int k,
-                                    hipStream_t stream, XAux aux) {
+bool gate_up_silu_q8_fits(int rows, int k) { return k == 2048 && gate_up_silu_waves(rows, k) == 8; }
+
+hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, void *act, int rows, int k,
+                                    hipStream_t stream, XAux aux, bool q8) {
     const int waves = gate_up_silu_waves(rows, k);
-    if ((xf != X_F32 && xf != X_RMS) || waves == 0) return hipErrorInvalidValue;
+    if ((xf != X_F32 && xf != X_RMS) || waves == 0 || (q8 && !gate_up_silu_q8_fits(rows, k)))
+        return hipErrorInvalidValue;
     GemvParams P{};
-    derive_plain(P, w, x, act, rows, k);
+    derive_plain(P, w, x, static_cast<float *>(act), rows, k);
     P.norm_w = aux.norm_w;
     P.eps = aux.eps;
     const int half = P.tiles / 2;
@@ -218,8 +221,12 @@ hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf
     const int grid = half / (waves / 2);
     const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? rms_sq_doubles(k) * 8 + 16 : 0);
     const size_t lds = (size_t)waves * TILE_BYTES + x_lds;
-    if (xf == X_RMS) return launch_pass<X_RMS, true, true, false, true>(P, grid, 64 * waves, lds, stream);
-    return launch_pass<X_F32, true, true, false, true>(P, grid, 64 * waves, lds, stream);
+    if (q8) {
+        if (xf == X_RMS) return launch_pass<X_RMS, true, true, false, PAIR_Q8>(P, grid, 64 * waves, lds, stream);
+        return launch_pass<X_F32, true, true, false, PAIR_Q8>(P, grid, 64 * waves, lds, stream);
+    }
+    if (xf == X_RMS) return launch_pass<X_RMS, true, true, false, PAIR_F32>(P, grid, 64 * waves, lds, stream);
+    return launch_pass<X_F32, true, true, false, PAIR_F32>(P, grid, 64 * waves, lds, stream);
 }
 
 hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream) {

@@ -249,15 +249,21 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
 // the others the matching up tiles, one tile each (the grid is exactly
 // tiles / 2 / V workgroups). A gate wave leaves its rows' y in its slab, and
 // after a workgroup barrier its partner stores act[r] = silu_mul(gate, up)
-// to y[0 .. rows / 2).
+// to y[0 .. rows / 2) (PAIR_F32). PAIR_Q8: act quantized to Q8_0 in the
+// epilogue instead, y the engine layout of act (int8[n] | float32[n / 32],
+// n = rows / 2), the input of down as the reference's caller quantizes it
+// (tp_llama.cpp:330-352). Needs V * rpw = 32 (k = 2048, V = 4): a
+// workgroup's outputs are then exactly Q8_0 block b of act, quantized by
+// eight lanes of its first up wave as the fused activation quantizer does.
 // COH (the chain plan's dispatches, which carry no cache fences between
 // them): bit 0, x is an earlier step's output, read from the device's
 // coherence point (past the L2 of this XCD); bit 1, y is a later step's x,
 // written through to it and waited for before the wave ends. ONE_PASS (and
-// PAIR) only; fp32 x formats only.
+// PAIR) only; fp32 and engine-layout x formats.
 constexpr int COH_X = 1, COH_Y = 2;
+constexpr int PAIR_F32 = 1, PAIR_Q8 = 2;
 
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false, int COH = 0>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, int PAIR = 0, int COH = 0>
 __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, int nthreads, uint8_t *lds) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
@@ -353,7 +359,8 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     const int acc_r = lane >> 3, acc_a = lane & 7;
     unsigned long long best = 0;          // argmax epilogue: this lane's best key
     const __amdgpu_buffer_rsrc_t y_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * (PAIR ? P.rows / 2 : P.rows), BUFFER_DWORD3);
+        __builtin_amdgcn_make_buffer_rsrc(P.y, 0, PAIR == PAIR_Q8 ? P.rows / 2 + P.rows / 16 : 4 * (PAIR ? P.rows / 2 : P.rows),
+                                          BUFFER_DWORD3);
     // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
     // slab -> ordered lane sums -> tree -> y; with REFILL the buffer then
     // receives the tile DEPTH strides ahead while the terms are computed.
@@ -398,11 +405,43 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             const bool mine = acc_r < rpw && acc_a == 0;
             if (!up_wave && mine) s_t[acc_r] = yv;
             __syncthreads();
-            if (up_wave) {
-                const float gate = reinterpret_cast<const float *>(lds + (size_t)(wave - pv) * TILE_BYTES)[acc_r < rpw ? acc_r : 0];
-                const int row = (tile - (P.tiles >> 1)) * rpw + acc_r;
-                const float act = silu_mul(gate, yv);
-                store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, mine && row < (P.rows >> 1) ? 4 * row : OUT_OF_RANGE, act);
+            if constexpr (PAIR == PAIR_F32) {
+                if (up_wave) {
+                    const float gate = reinterpret_cast<const float *>(lds + (size_t)(wave - pv) * TILE_BYTES)[acc_r < rpw ? acc_r : 0];
+                    const int row = (tile - (P.tiles >> 1)) * rpw + acc_r;
+                    const float act = silu_mul(gate, yv);
+                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, mine && row < (P.rows >> 1) ? 4 * row : OUT_OF_RANGE, act);
+                }
+            } else {
+                // The block's 32 act values go to the first floats of the
+                // first up wave's slab (its sums are done: the barrier above
+                // came after them), in row order; after a second barrier its
+                // lanes 0..7 quantize four each, amax met over the eight by
+                // DPP, exactly as a thread holding the whole block would
+                // (quantize.hip's quantize_store8).
+                float *s_q = reinterpret_cast<float *>(lds + (size_t)pv * TILE_BYTES);
+                if (up_wave && mine) {
+                    const float gate = reinterpret_cast<const float *>(lds + (size_t)(wave - pv) * TILE_BYTES)[acc_r];
+                    s_q[(wave - pv) * rpw + acc_r] = silu_mul(gate, yv);
+                }
+                __syncthreads();
+                if (wave == pv && lane < 8) {
+                    const float4 v = reinterpret_cast<const float4 *>(s_q)[lane];
+                    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+                    amax = fmaxf(amax, dpp_mov<0xB1>(amax));
+                    amax = fmaxf(amax, dpp_mov<0x4E>(amax));
+                    amax = fmaxf(amax, dpp_mov<0x141>(amax));
+                    const float d = q8_scale(amax);
+                    const float inv = safe_recip(d);
+                    const uint32_t word = (uint32_t)(uint8_t)q8_round(v.x, inv) |
+                                          ((uint32_t)(uint8_t)q8_round(v.y, inv) << 8) |
+                                          ((uint32_t)(uint8_t)q8_round(v.z, inv) << 16) |
+                                          ((uint32_t)(uint8_t)q8_round(v.w, inv) << 24);
+                    const int n = P.rows >> 1;
+                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, 32 * block + 4 * lane, __uint_as_float(word));
+                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, lane == 0 ? n + 4 * block : OUT_OF_RANGE,
+                                                     half_bits_to_float(float_to_half_bits(d)));
+                }
             }
         } else if constexpr (ONE_PASS) {
             const float yv = tree8_dpp(lane_sum(acc_r));
@@ -465,7 +504,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
 // nothing of the block, in 277 (the same as with nothing preloaded), and
 // delaying the weight loads by other means (a sleep, or a wait for the
 // activation's loads) did not recover it.
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, bool PAIR = false>
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, int PAIR = 0>
 __global__ __launch_bounds__(MAX_THREADS) void gemv_m1_kernel(const uint8_t *w0, const void *x, int rows, int k, int C,
                                                               int rpw, int tiles, int nblocks, int nthreads,
                                                               GemvParams P) {

@@ -77,9 +77,9 @@ __device__ __forceinline__ void x_load(const void *x, int k, int b, bool live, X
     } else if constexpr (XF == X_ENGINE) {
         const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(k + k / 8));
         const int q_off = live ? 32 * b : OUT_OF_RANGE, d_off = live ? k + 4 * b : OUT_OF_RANGE;
-        r.q0 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off, 0, 0);
-        r.q1 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off + 16, 0, 0);
-        r.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xb, d_off, 0, 0));
+        r.q0 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off, 0, AUX);
+        r.q1 = __builtin_amdgcn_raw_buffer_load_b128(xb, q_off + 16, 0, AUX);
+        r.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xb, d_off, 0, AUX));
     } else if constexpr (XF == X_Q8_0) {
         const uint16_t *src = reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(x) +
                                                                  Q8_0_BYTES * (live ? b : 0));

@@ -130,10 +130,15 @@ int chain_mode();
 hipError_t launch_gemv_batch(const w4a8_chain_step *steps, int n, hipStream_t stream);
 // gate|up (rows = 2 n) with silu(gate) * up as the epilogue: act[n] from
 // x as X_F32 or X_RMS (aux), 2048 <= k <= 8192, n a multiple of 64 / (k / 256).
-hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, float *act, int rows, int k,
-                                    hipStream_t stream, XAux aux = XAux{});
+// q8: act quantized in the epilogue, `act` then the engine layout of n values
+// (gate_up_silu_q8_fits).
+hipError_t launch_gemv_gate_up_silu(const uint8_t *w, const float *x, XFormat xf, void *act, int rows, int k,
+                                    hipStream_t stream, XAux aux = XAux{}, bool q8 = false);
 // Its workgroup size in waves for a shape, 0 when the shape does not fit.
 int gate_up_silu_waves(int rows, int k);
+// The quantizing form needs a workgroup's 32 outputs to be one Q8_0 block:
+// k = 2048 and eight waves.
+bool gate_up_silu_q8_fits(int rows, int k);
 
 // w: float32[rows][K] -> Q4_0 rows.
 hipError_t launch_quantize_q4_0(const float *w, int rows, int k, uint8_t *out, hipStream_t stream);

@@ -42,6 +42,7 @@ EXPORTS = (
     "w4a8_chain_gemv", "w4a8_gemv_batch", "w4a8_argmax_workspace_bytes", "w4a8_gemv_f32_argmax",
     "w4a8_gemv_rmsnorm", "w4a8_gemv_rmsnorm_argmax", "w4a8_gemv_silu_mul", "w4a8_rmsnorm_q8_0",
     "w4a8_silu_mul_q8_0", "w4a8_topk_workspace_bytes", "w4a8_topk", "w4a8_topk_no_alloc", "w4a8_gemv_gate_up_silu",
+    "w4a8_gemv_gate_up_silu_q8_0",
     "w4a8_chain_set_mode", "w4a8_chain_set_spin_limit", "w4a8_chain_timeouts",
     "w4a8_chain_plan_create", "w4a8_chain_plan_create_steps", "w4a8_chain_plan_launch", "w4a8_chain_plan_wait",
     "w4a8_chain_plan_destroy",
@@ -127,6 +128,8 @@ def lib() -> ctypes.CDLL:
     L.w4a8_topk_no_alloc.restype = i
     L.w4a8_gemv_gate_up_silu.argtypes = [p, p, p, f32, p, i, i, p]
     L.w4a8_gemv_gate_up_silu.restype = i
+    L.w4a8_gemv_gate_up_silu_q8_0.argtypes = [p, p, p, f32, p, i, i, p]
+    L.w4a8_gemv_gate_up_silu_q8_0.restype = i
     for f in ("w4a8_chain_gemv", "w4a8_gemv_batch"):
         getattr(L, f).argtypes = [p, i, p]
         getattr(L, f).restype = i
@@ -147,7 +150,7 @@ def lib() -> ctypes.CDLL:
     return L
 
 
-PLAN_GEMV, PLAN_GATE_UP_SILU, PLAN_ARGMAX = 0, 1, 2
+PLAN_GEMV, PLAN_GATE_UP_SILU, PLAN_ARGMAX, PLAN_GATE_UP_SILU_Q8, PLAN_GEMV_ENGINE = 0, 1, 2, 3, 4
 
 
 class PlanStep(ctypes.Structure):
@@ -353,10 +356,12 @@ def argmax_workspace():
     return torch.zeros(lib().w4a8_argmax_workspace_bytes(), dtype=torch.uint8, device="cuda")
 
 
-def gemv_gate_up_silu(blocks, k: int, x, norm_w=None, eps: float = 1e-5, out=None):
+def gemv_gate_up_silu(blocks, k: int, x, norm_w=None, eps: float = 1e-5, out=None, q8: bool = False):
     """act = silu(gate) * up of the gate|up GEMV y = W Q8_0(rmsnorm(x) * norm_w)
     (or of x itself when norm_w is None), rows = 2n gate rows then up rows:
-    float32 [n], in one kernel (board/tp/tp_llama.cpp:557-569, 612-619)."""
+    float32 [n], in one kernel (board/tp/tp_llama.cpp:557-569, 612-619).
+    q8: act quantized in the same kernel, returned in the engine layout
+    (uint8 [n + n/8], the input of gemv_engine; k = 2048 only)."""
     import torch
     _need(x, torch.float32, "x")
     _check_blocks(blocks, k)
@@ -371,8 +376,13 @@ def gemv_gate_up_silu(blocks, k: int, x, norm_w=None, eps: float = 1e-5, out=Non
         if tuple(norm_w.shape) != (k,):
             raise ValueError(f"norm_w must be [{k}], got {tuple(norm_w.shape)}")
         _same_device(norm_w, blocks, "norm_w")
-    act = _out(out, (rows // 2,), torch.float32, blocks)
-    check("w4a8_gemv_gate_up_silu", lib().w4a8_gemv_gate_up_silu(
+    if q8:
+        act = _out(out, (engine_x_bytes(rows // 2),), torch.uint8, blocks)
+        fn = "w4a8_gemv_gate_up_silu_q8_0"
+    else:
+        act = _out(out, (rows // 2,), torch.float32, blocks)
+        fn = "w4a8_gemv_gate_up_silu"
+    check(fn, getattr(lib(), fn)(
         blocks.data_ptr(), x.data_ptr(), None if norm_w is None else norm_w.data_ptr(), float(eps), act.data_ptr(),
         rows, k, _stream(blocks)))
     return act

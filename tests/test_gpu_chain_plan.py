@@ -294,6 +294,39 @@ def test_plan_producer_steps_match_the_stream_entry_points(gpu):
         assert not ws.any().item(), "the argmax step leaves its workspace zero"
 
 
+def test_plan_quantized_act_into_down(gpu):
+    """gate|up quantizing its act in the epilogue (W4A8_PLAN_GATE_UP_SILU_Q8)
+    and down on that engine-layout act (W4A8_PLAN_GEMV_ENGINE), in one pass
+    and over three: both outputs against the stream entry points and the
+    oracle."""
+    import torch
+    k, n_ff = 2048, 8192
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    resid = torch.randn(k, generator=g, device="cuda")
+    norm = torch.randn(k, generator=g, device="cuda")
+    gu, down = _blocks(2 * n_ff, k, 31), _blocks(k, n_ff, 32)
+    for nw in (norm, None):
+        want_act = gpu.gemv_gate_up_silu(gu, k, resid, nw, 1e-5, q8=True)
+        want_down = gpu.gemv_engine(down, n_ff, want_act)
+        want_down_f32 = gpu.gemv_q4_0_f32(down, n_ff, gpu.gemv_gate_up_silu(gu, k, resid, nw, 1e-5))
+        torch.cuda.synchronize()
+        assert_bytes_equal(host(want_down), host(want_down_f32), "down on the quantized act = down on the fp32 act")
+        act = torch.full((gpu.engine_x_bytes(n_ff),), 0xAA, dtype=torch.uint8, device="cuda")
+        y = poisoned_f32(k)
+        S = gpu.PlanStep
+        steps = [S(gpu.PLAN_GATE_UP_SILU_Q8, gu.data_ptr(), resid.data_ptr(), act.data_ptr(), 2 * n_ff, k,
+                   None if nw is None else nw.data_ptr(), 1e-5),
+                 S(gpu.PLAN_GEMV_ENGINE, down.data_ptr(), act.data_ptr(), y.data_ptr(), k, n_ff, None, 0.0)]
+        for passes in (1, 3):
+            act.fill_(0xAA)
+            y.fill_(float("nan"))
+            _run_steps(gpu, steps, passes)
+            tag = f"{'rmsnorm' if nw is not None else 'plain'}, {passes} passes"
+            assert torch.equal(act, want_act), f"{tag}: act"
+            assert_bytes_equal(host(y), host(want_down), f"{tag}: down")
+
+
 def test_plan_steps_argument_checks(gpu):
     import torch
     L = gpu.lib()
@@ -309,6 +342,10 @@ def test_plan_steps_argument_checks(gpu):
     assert create(S(7, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 2048, None, 0.0)) == -2       # kind
     assert create(S(gpu.PLAN_ARGMAX, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 2048, None, 0.0)) == -1
     assert create(S(gpu.PLAN_GATE_UP_SILU, w.data_ptr(), x.data_ptr(), y.data_ptr(), 6, 2048, None, 0.0)) == -2
+    assert create(S(gpu.PLAN_GATE_UP_SILU_Q8, w.data_ptr(), x.data_ptr(), y.data_ptr(), 16, 2048, None, 0.0)) == -2
+    assert create(S(gpu.PLAN_GEMV_ENGINE, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 2048, x.data_ptr(),
+                    1e-5)) == -2                                                                  # no rmsnorm on engine x
+    assert create(S(5, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 2048, None, 0.0)) == -2        # kind
     w16 = _blocks(64, 16384, 22)
     x16 = torch.zeros(16384, device="cuda")
     assert create(S(gpu.PLAN_GEMV, w16.data_ptr(), x16.data_ptr(), y.data_ptr(), 64, 16384, x16.data_ptr(),

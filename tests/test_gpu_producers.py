@@ -128,6 +128,49 @@ def test_gemv_gate_up_silu(gpu, rows, k, rms):
     assert_bytes_equal(host(got), want, f"gate_up_silu {rows}x{k}")
 
 
+@pytest.mark.parametrize("rows,rms", [(16384, True), (16384, False), (64, True), (192, False)])
+def test_gemv_gate_up_silu_q8_0(gpu, rows, rms):
+    """gate|up with silu(gate) * up quantized in the epilogue: the engine
+    layout of Q8_0(silu_mul(y[:n], y[n:])), byte for byte, and down on it
+    equal to down on the fp32 act (its own fused quantize)."""
+    import torch
+    k = 2048
+    print(f"gate_up_silu_q8_0 rows={rows} rms={rms}", flush=True)
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 190 + rows, 0.02))
+    rng = np.random.default_rng(rows + 7)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    w = rng.standard_normal(k).astype(np.float32) if rms else None
+    h = C.rmsnorm(x, w, 1e-5) if rms else x
+    xq, xd = C.quantize_q8_0(h)
+    y = C.gemv_q4_0(blocks, k, xq, xd)
+    n = rows // 2
+    act = C.silu_mul(y[:n], y[n:])
+    want = _engine(act)
+    got = gpu.gemv_gate_up_silu(dev(blocks), k, dev(x), None if w is None else dev(w), 1e-5, q8=True)
+    assert_bytes_equal(host(got), want, f"gate_up_silu_q8_0 {rows}x{k}")
+    if n >= 256:
+        down = C.quantize_q4_0(O.normal_f32((256, n), 300 + rows, 0.02))
+        aq, ad = C.quantize_q8_0(act)
+        y_down = gpu.gemv_engine(dev(down), n, got)
+        assert_bytes_equal(host(y_down), C.gemv_q4_0(down, n, aq, ad), "down on the quantized act")
+    torch.cuda.synchronize()
+
+
+def test_gemv_gate_up_silu_q8_0_rejects(gpu):
+    import torch
+    L = gpu.lib()
+    w = torch.zeros(64 * 4096 // 32 * 18, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    act = torch.zeros(256, dtype=torch.uint8, device="cuda")
+    call = lambda rows, k, a=act: L.w4a8_gemv_gate_up_silu_q8_0(w.data_ptr(), x.data_ptr(), None, 1e-5, a.data_ptr(),
+                                                                 rows, k, None)
+    assert call(64, 4096) == -2        # k = 4096: 16 rows per workgroup, not a Q8_0 block
+    assert call(16, 2048) == -2        # one tile per half: no workgroup of four gate tiles
+    assert call(48, 2048) == -2        # three tiles per half
+    assert call(64, 2048, act[4:]) == -3   # act not 16-byte aligned
+    torch.cuda.synchronize()
+
+
 def test_gemv_gate_up_silu_rejects(gpu):
     import torch
     L = gpu.lib()
