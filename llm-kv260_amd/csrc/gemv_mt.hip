@@ -12,12 +12,15 @@
 //    LDS slab, so that lane l holds chunk l (eight consecutive blocks of a
 //    row, 144 bytes).
 //  * A lane pulls its eight blocks' fp16 scales and packed nibbles out of the
-//    chunk once, with the nibble sums that v_dot8_u32_u4's form of the block
-//    dot needs (block_dot_nib, q4_0_device.h), and keeps them for every token.
+//    chunk once; each block's nibbles are unpacked to bytes once and meet
+//    every token's int8 values in v_dot4_i32_i8 block dots (block_dot_raw,
+//    q4_0_device.h: eight dots per block and token, where the M = 1 GEMV's
+//    nibble-split form takes twelve and two integer ops).
 //  * Per token it reads its chunk column of that token's staged activation
-//    (LDS, one copy per token, the layout x_stage writes) and computes the
-//    eight terms (f32(sumi) * d_w) * d_x, then the contract's ordered lane
-//    sums and adjacent-pair tree through the slab, exactly as for M = 1.
+//    (LDS, one copy per token, the layout x_stage writes, with the int8
+//    values as they are) and computes the eight terms (f32(sumi) * d_w) *
+//    d_x, then the contract's ordered lane sums and adjacent-pair tree
+//    through the slab, exactly as for M = 1.
 // The activation rows are staged once per workgroup, their loads issued
 // before the first weight tile's so that the staging waits for them only.
 #include <atomic>
@@ -63,25 +66,28 @@ __device__ __forceinline__ void mt_load_tile(const MtParams &P, int tile, int la
     for (int p = 0; p < CHUNK_PIECES; ++p) t.p[p] = __builtin_amdgcn_raw_buffer_load_b128(tb, 1024 * p + 16 * lane, 0, CACHE_NT);
 }
 
-// sum(n) of one block's 32 unsigned nibbles: the token-independent term of
-// block_dot_nib, computed once per block and kept for every token.
-__device__ __forceinline__ uint32_t nibble_sum(const uint32_t qs[4]) {
-    uint32_t n = 0;
+// The eight block terms of this lane's chunk for TG tokens t0 .. t0 + TG - 1
+// (a token past m reads token `past` instead and is never stored): each
+// block's weights unpacked to bytes once, then one v_dot4 block dot per token
+// (block_dot_raw) on the token's staged int8 values, and the contract's term.
+template <int TG>
+__device__ __forceinline__ void mt_terms(const uint32_t qs[8][4], const uint32_t dw[8], const uint32_t *s_x,
+                                         int tok_dwords, int colx, int t0, int m, float term[TG][8], int past = -1) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) n = __builtin_amdgcn_udot8(qs[k], 0x11111111u, n, false);
-    return n;
-}
-
-// block_dot_nib with sum(n) given: the same terms, so the same int32.
-__device__ __forceinline__ int32_t block_dot_with_sum(const uint32_t qs[4], uint32_t n, const uint32_t xn[8],
-                                                      int32_t c8) {
-    uint32_t a = 0, b = (uint32_t)c8;
+    for (int j = 0; j < 8; ++j) {
+        uint32_t lo[4], hi[4];
+        unpack_nibbles(qs[j], lo, hi);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        a = __builtin_amdgcn_udot8(qs[k], xn[k], a, false);
-        b = __builtin_amdgcn_udot8(qs[k], xn[4 + k], b, false);
+        for (int u = 0; u < TG; ++u) {
+            const int t = t0 + u < m ? t0 + u : (past < 0 ? t0 : past);
+            const uint32_t *col = s_x + t * tok_dwords + colx * XCOL_DWORDS;
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(col + 8 * j);
+            const u32x4 a = src[0], c = src[1];
+            const uint32_t xr[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            const int32_t sumi = block_dot_raw(lo, hi, xr, (int32_t)col[XCOL_S + j]);
+            term[u][j] = block_term(sumi, dw[j], __uint_as_float(col[XCOL_D + j]));
+        }
     }
-    return (int32_t)(16u * a + b) - 128 * (int32_t)n;
 }
 
 // PASSES: staging rounds of blocks per thread, m * nb <= PASSES * threads.
@@ -121,7 +127,7 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
         for (int p = 0; p < PASSES; ++p) {
             const int i = tid + p * nthreads;
             const int t = i / nb, b = i - t * nb;
-            if (t < P.m) x_stage<X_ENGINE>(xr[p], b, s_x + t * tok_dwords);
+            if (t < P.m) x_stage<X_ENGINE, true>(xr[p], b, s_x + t * tok_dwords);
         }
         __syncthreads();
     };
@@ -148,10 +154,8 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
             }
         }
         if (refill) mt_load_tile(P, tile + 2 * tstride, lane, bt);
-        uint32_t qs[8][4], dw[8], ns[8];
-#define W4A8_BLK(J)                           \
-    chunk_block<J>(w, dw[J], qs[J]);          \
-    ns[J] = nibble_sum(qs[J]);
+        uint32_t qs[8][4], dw[8];
+#define W4A8_BLK(J) chunk_block<J>(w, dw[J], qs[J]);
         W4A8_BLK(0) W4A8_BLK(1) W4A8_BLK(2) W4A8_BLK(3) W4A8_BLK(4) W4A8_BLK(5) W4A8_BLK(6) W4A8_BLK(7)
 #undef W4A8_BLK
         float *s_t = reinterpret_cast<float *>(slab);
@@ -162,19 +166,7 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
         // pair of syncs.
         for (int t0 = 0; t0 < P.m; t0 += TG) {
             float term[TG][8];
-#pragma unroll
-            for (int u = 0; u < TG; ++u) {
-                const int t = t0 + u < P.m ? t0 + u : t0;   // past m: t0 again, never stored
-                const uint32_t *col = s_x + t * tok_dwords + colx * XCOL_DWORDS;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const u32x4 *src = reinterpret_cast<const u32x4 *>(col + 8 * j);
-                    const u32x4 a = src[0], c = src[1];
-                    const uint32_t xn[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-                    const int32_t sumi = block_dot_with_sum(qs[j], ns[j], xn, (int32_t)col[XCOL_S + j]);
-                    term[u][j] = block_term(sumi, dw[j], __uint_as_float(col[XCOL_D + j]));
-                }
-            }
+            mt_terms<TG>(qs, dw, s_x, tok_dwords, colx, t0, P.m, term);
             wave_sync_lds();
 #pragma unroll
             for (int u = 0; u < TG; ++u)
@@ -291,7 +283,7 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
     for (int p = 0; p < PASSES; ++p) {
         const int i = tid + p * nthreads;
         const int t = i / nb, b = i - t * nb;
-        if (t < P.m) x_stage<X_ENGINE>(xr[p], b, s_x + t * tok_dwords);
+        if (t < P.m) x_stage<X_ENGINE, true>(xr[p], b, s_x + t * tok_dwords);
     }
     {
         u32x4 *wslab = reinterpret_cast<u32x4 *>(slab);
@@ -312,10 +304,8 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
         }
     }
     __syncthreads();   // both chunks pulled: the slab takes wave 0's terms
-    uint32_t qs[8][4], dw[8], ns[8];
-#define W4A8_BLK(J)                           \
-    chunk_block<J>(w, dw[J], qs[J]);          \
-    ns[J] = nibble_sum(qs[J]);
+    uint32_t qs[8][4], dw[8];
+#define W4A8_BLK(J) chunk_block<J>(w, dw[J], qs[J]);
     W4A8_BLK(0) W4A8_BLK(1) W4A8_BLK(2) W4A8_BLK(3) W4A8_BLK(4) W4A8_BLK(5) W4A8_BLK(6) W4A8_BLK(7)
 #undef W4A8_BLK
 
@@ -323,19 +313,7 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
     // in as few passes as the lanes allow (8 rpw lanes per token).
     const int t0 = half * TG;
     float term[TG][8];
-#pragma unroll
-    for (int u = 0; u < TG; ++u) {
-        const int t = t0 + u < P.m ? t0 + u : 0;          // past m: token 0 again, never stored
-        const uint32_t *col = s_x + t * tok_dwords + colx * XCOL_DWORDS;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(col + 8 * j);
-            const u32x4 a = src[0], c = src[1];
-            const uint32_t xn[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-            const int32_t sumi = block_dot_with_sum(qs[j], ns[j], xn, (int32_t)col[XCOL_S + j]);
-            term[u][j] = block_term(sumi, dw[j], __uint_as_float(col[XCOL_D + j]));
-        }
-    }
+    mt_terms<TG>(qs, dw, s_x, tok_dwords, colx, t0, P.m, term, 0);
 #pragma unroll
     for (int u = 0; u < TG; ++u)
 #pragma unroll
@@ -405,17 +383,25 @@ int gemv_mt_max_m(int rows, int k) {
     (void)rows; (void)k;
     return W4A8_MT_MAX_ALL;
 #else
-    // Measured on MI355X against the MFMA kernels (rotated weights, us):
+    // Measured on MI355X against the MFMA kernels (rotated weights, us, with
+    // the v_dot4 block dots):
     //  * m = 2 on every shape (q|k|v 4.3 against 4.9, o 4.2 against 4.8,
-    //    gate|up 6.7 against 8.4, down 5.5 against 9.5);
-    //  * m = 3, 4 from K = 4096 or 8,192 rows on (4096 x 4096 6.0-6.1
-    //    against 6.9, gate|up 8.0-8.1 against 8.3-8.4, 8192 x 2048 5.9
-    //    against 6.4, down 6.8-6.9 against 9.3-9.4); below that even;
-    //  * m = 5, 6 at K = 8192 where a tile's tokens are split over two waves
-    //    (down 8.1-8.2 against 9.3); at m = 7, 8 the two are even.
+    //    gate|up 6.6 against 8.4, down 5.5 against 9.5);
+    //  * m = 3, 4 from K = 4096 or 8,192 rows on (4096 x 4096 5.8-5.9
+    //    against 6.9, gate|up 8.0-8.1 against 8.3-8.4, 8192 x 2048 5.6-5.7
+    //    against 6.4, down 6.5-6.6 against 9.3-9.4); below that slower
+    //    (q|k|v 5.0-5.1 against 4.9);
+    //  * where a tile's tokens are split over two waves (at most four tiles
+    //    per CU): m <= 8 at K = 8192 (down 7.6 at m = 5, 6 and 8.2-8.3 at
+    //    m = 7, 8, against 9.3-9.4), m <= 6 at K = 2048 (8192 x 2048 6.5
+    //    against 6.9 at m = 5, 6; 7.2 against 7.0 at m = 7, 8); 4096 x 4096
+    //    even at m = 5, 6.
     const int rpw = 64 / (k / 256 > 0 ? k / 256 : 1);
     const int tiles = (rows + rpw - 1) / rpw;
-    if (k >= 8192 && W4A8_MT_SPLIT && tiles <= 4 * device_cu_count()) return 6;
+    if (W4A8_MT_SPLIT && tiles <= 4 * device_cu_count()) {
+        if (k >= 8192) return 8;
+        if (k == 2048 && rows >= 8192) return 6;
+    }
     if (rows >= 8192 || k >= 4096) return 4;
     return 2;
 #endif

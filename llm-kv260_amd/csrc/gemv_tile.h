@@ -108,9 +108,10 @@ constexpr int XCOL_D = 64;     // the scales' offset in a column
 constexpr int XCOL_S = 72;     // the corrections'
 __host__ __device__ constexpr size_t x_lds_bytes(int nb) { return (size_t)(nb / 8) * XCOL_DWORDS * 4; }
 
-// Quantize (if fp32) and store block b into LDS: its values as nibbles, its
-// fp32 scale, and -8 times the sum of its int8 values.
-template <int XF>
+// Quantize (if fp32) and store block b into LDS: its values as nibbles (RAW:
+// as the int8 values themselves, for block_dot_raw), its fp32 scale, and -8
+// times the sum of its int8 values.
+template <int XF, bool RAW = false>
 __device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_x, float rms_scale = 0.0f) {
     uint32_t q[8];
     float dx;
@@ -168,7 +169,12 @@ __device__ __forceinline__ void x_stage(const XRaw<XF> &r, int b, uint32_t *s_x,
 #pragma unroll
     for (int m = 0; m < 8; ++m) sum = __builtin_amdgcn_sdot4((int)q[m], 0x01010101, sum, false);
     uint32_t xn[8];
-    x_nibbles(q, xn);
+    if constexpr (RAW) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) xn[m] = q[m];
+    } else {
+        x_nibbles(q, xn);
+    }
     uint32_t *col = s_x + (b >> 3) * XCOL_DWORDS;
     const int j = b & 7;
     u32x4 *dst = reinterpret_cast<u32x4 *>(col + 8 * j);

@@ -66,6 +66,33 @@ __device__ __forceinline__ int32_t block_dot_nib(const uint32_t qs[4], const uin
     return (int32_t)(16u * a + b) - 128 * (int32_t)n;
 }
 
+// The same exact int32 for a block whose activation is given as its int8
+// values (xr[m]: x[4m .. 4m + 3]) and whose weights are unpacked to bytes
+// (unpack_nibbles: lo[k] = weights 4k .. 4k + 3, the low nibbles of dword k;
+// hi[k] = weights 16 + 4k .., its high nibbles), each an unsigned byte 0..15
+// that v_dot4_i32_i8 multiplies by the signed x; c8 = -8 sum(x) makes the sum
+// that of (n - 8) x. Eight dots per block and activation, against
+// block_dot_nib's twelve dots and two integer ops on a nibble-split x: the
+// cheaper form where one unpacked block meets several activations.
+__device__ __forceinline__ void unpack_nibbles(const uint32_t qs[4], uint32_t lo[4], uint32_t hi[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        lo[k] = qs[k] & 0x0F0F0F0Fu;
+        hi[k] = (qs[k] >> 4) & 0x0F0F0F0Fu;
+    }
+}
+
+__device__ __forceinline__ int32_t block_dot_raw(const uint32_t lo[4], const uint32_t hi[4], const uint32_t xr[8],
+                                                 int32_t c8) {
+    int32_t acc = c8;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        acc = __builtin_amdgcn_sdot4((int)lo[k], (int)xr[k], acc, false);
+        acc = __builtin_amdgcn_sdot4((int)hi[k], (int)xr[4 + k], acc, false);
+    }
+    return acc;
+}
+
 // The activation of one block as block_dot_nib takes it, from its eight
 // dwords of int8 values (byte e of q[m] is x[4m + e]).
 __device__ __forceinline__ void x_nibbles(const uint32_t q[8], uint32_t xn[8]) {
