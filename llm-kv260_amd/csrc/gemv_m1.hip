@@ -93,7 +93,10 @@ M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool argmax, int cus) {
     // staged in one pass. (Spreading an fp32 x's quantization over 2-8
     // threads per block, in helper waves or in the spare threads of the
     // larger workgroups, made no launch faster: the down GEMV lost 0.9 us.)
-    const int min_waves = nb > 64 ? (nb + 63) / 64 : 1;     // <= 8 for K <= 16384
+    int min_waves = nb > 64 ? (nb + 63) / 64 : 1;           // <= 8 for K <= 16384
+    // The rmsnorm forms stage their x with four threads per block where a
+    // workgroup can hold them (K = 2048: four waves).
+    if (xf == X_RMS && nb / 16 <= MAX_THREADS / 64 && nb / 16 > min_waves) min_waves = nb / 16;
     int waves = min_waves;
     int grid = (tiles + waves - 1) / waves;
     if (tiles > 2 * cus) {

@@ -295,7 +295,18 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     // staging below waits for them only.
     XRaw<XF> xr;
     constexpr int XAUX = (COH & COH_X) ? SC1 : 0;
-    x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+    // X_RMS with four threads per block (every launch shape at K = 2048):
+    // each thread loads, squares and stages a quarter of a block.
+    [[maybe_unused]] XQuarter xq;
+    const bool quarter = XF == X_RMS && nthreads >= 4 * nb;
+    if constexpr (XF == X_RMS) {
+        if (quarter)
+            x_load_quarter<XAUX>(P.x, P.norm_w, P.k, tid >> 2, tid & 3, tid < 4 * nb, xq);
+        else
+            x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+    } else {
+        x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+    }
 
 
     uint32_t xv[8][8];
@@ -323,11 +334,26 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                     c0[3 * cs + m] = e * e;
                 }
             };
-            if (tid < nb) squares(xr, tid);
-            for (int b = tid + nthreads; b < nb; b += nthreads) {
-                XRaw<XF> xb;
-                x_load<XF, XAUX>(P.x, P.k, b, true, xb, P.norm_w);
-                squares(xb, b);
+            if (quarter) {
+                // Element 32 b + 4 q + c is square 8 b + q of chain c; element
+                // 32 b + 16 + 4 q + c square 8 b + 4 + q.
+                if (tid < 4 * nb) {
+                    double *c0 = sq + 8 * (tid >> 2) + (tid & 3);
+                    const double a[4] = {xq.xa.x, xq.xa.y, xq.xa.z, xq.xa.w};
+                    const double e[4] = {xq.xb.x, xq.xb.y, xq.xb.z, xq.xb.w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        c0[c * cs] = a[c] * a[c];
+                        c0[c * cs + 4] = e[c] * e[c];
+                    }
+                }
+            } else {
+                if (tid < nb) squares(xr, tid);
+                for (int b = tid + nthreads; b < nb; b += nthreads) {
+                    XRaw<XF> xb;
+                    x_load<XF, XAUX>(P.x, P.k, b, true, xb, P.norm_w);
+                    squares(xb, b);
+                }
             }
             __syncthreads();
             if (wave == 0) {
@@ -337,11 +363,17 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             __syncthreads();
             rms = *s_rms;
         }
-        if (tid < nb) x_stage<XF>(xr, tid, s_x, rms);
-        for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
-            XRaw<XF> xb;
-            x_load<XF, XAUX>(P.x, P.k, b, true, xb, P.norm_w);
-            x_stage<XF>(xb, b, s_x, rms);
+        if (quarter) {
+            if constexpr (XF == X_RMS) {
+                if (tid < 4 * nb) x_stage_quarter(xq, tid >> 2, tid & 3, s_x, rms);
+            }
+        } else {
+            if (tid < nb) x_stage<XF>(xr, tid, s_x, rms);
+            for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
+                XRaw<XF> xb;
+                x_load<XF, XAUX>(P.x, P.k, b, true, xb, P.norm_w);
+                x_stage<XF>(xb, b, s_x, rms);
+            }
         }
         __syncthreads();
         const uint32_t *col = s_x + (lane_live ? my_c : 0) * XCOL_DWORDS;

@@ -108,6 +108,70 @@ constexpr int XCOL_D = 64;     // the scales' offset in a column
 constexpr int XCOL_S = 72;     // the corrections'
 __host__ __device__ constexpr size_t x_lds_bytes(int nb) { return (size_t)(nb / 8) * XCOL_DWORDS * 4; }
 
+// A quarter of an fp32 block for the rmsnorm staging spread over four
+// threads: thread q of block b holds its elements 4q .. 4q + 3 (a) and
+// 16 + 4q .. 16 + 4q + 3 (b), exactly the int8 values of dwords q and 4 + q
+// of the staged block, which x_nibbles pairs into nibble dwords q and 4 + q.
+struct XQuarter {
+    float4 xa, xb, wa, wb;
+};
+
+template <int AUX = 0>
+__device__ __forceinline__ void x_load_quarter(const void *x, const float *norm_w, int k, int b, int q, bool live,
+                                               XQuarter &r) {
+    const __amdgpu_buffer_rsrc_t xr = buffer_of(x, (uint32_t)(4 * k));
+    const __amdgpu_buffer_rsrc_t wr = buffer_of(norm_w, (uint32_t)(4 * k));
+    const int off = live ? 128 * b + 16 * q : OUT_OF_RANGE;
+    const int off2 = live ? off + 64 : OUT_OF_RANGE;
+    auto f4 = [](u32x4 t) { return make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w)); };
+    r.xa = f4(__builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, AUX));
+    r.xb = f4(__builtin_amdgcn_raw_buffer_load_b128(xr, off2, 0, AUX));
+    r.wa = f4(__builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+    r.wb = f4(__builtin_amdgcn_raw_buffer_load_b128(wr, off2, 0, 0));
+}
+
+// The rmsnorm block's staging by its four threads (lanes 4b' .. 4b' + 3 of a
+// wave, an aligned quad): out = (x * scale) * w for their eight elements, the
+// block's amax met over the quad by DPP, the contract's Q8_0 rounding of each
+// element, and -8 * sum(x) summed over the quad; each thread stores its two
+// nibble dwords, thread 0 the scale and the correction. The same bytes as
+// x_stage<X_RMS> on the whole block in one thread.
+__device__ __forceinline__ void x_stage_quarter(const XQuarter &r, int b, int q, uint32_t *s_x, float rms_scale) {
+    const float xv[8] = {r.xa.x, r.xa.y, r.xa.z, r.xa.w, r.xb.x, r.xb.y, r.xb.z, r.xb.w};
+    const float wv[8] = {r.wa.x, r.wa.y, r.wa.z, r.wa.w, r.wb.x, r.wb.y, r.wb.z, r.wb.w};
+    float v[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float a = xv[e] * rms_scale;
+        v[e] = a * wv[e];
+        amax = fmaxf(amax, fabsf(v[e]));
+    }
+    amax = fmaxf(amax, dpp_mov<0xB1>(amax));   // quad_perm(1,0,3,2)
+    amax = fmaxf(amax, dpp_mov<0x4E>(amax));   // quad_perm(2,3,0,1)
+    const float d = q8_scale(amax);
+    const float inv = safe_recip(d);
+    uint32_t wlo = 0, whi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        wlo |= ((uint32_t)(uint8_t)q8_round(v[e], inv)) << (8 * e);
+        whi |= ((uint32_t)(uint8_t)q8_round(v[4 + e], inv)) << (8 * e);
+    }
+    int32_t sum = __builtin_amdgcn_sdot4((int)wlo, 0x01010101, 0, false);
+    sum = __builtin_amdgcn_sdot4((int)whi, 0x01010101, sum, false);
+    sum += __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, false);
+    sum += __builtin_amdgcn_mov_dpp(sum, 0x4E, 0xF, 0xF, false);
+    const uint32_t lo = wlo ^ 0x80808080u, hi = whi ^ 0x80808080u;   // x + 128, bytewise (x_nibbles)
+    uint32_t *col = s_x + (b >> 3) * XCOL_DWORDS;
+    const int j = b & 7;
+    col[8 * j + q] = ((lo >> 4) & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
+    col[8 * j + 4 + q] = (lo & 0x0F0F0F0Fu) | ((hi << 4) & 0xF0F0F0F0u);
+    if (q == 0) {
+        col[XCOL_D + j] = __float_as_uint(half_bits_to_float(float_to_half_bits(d)));
+        col[XCOL_S + j] = (uint32_t)(-8 * sum);
+    }
+}
+
 // Quantize (if fp32) and store block b into LDS: its values as nibbles (RAW:
 // as the int8 values themselves, for block_dot_raw), its fp32 scale, and -8
 // times the sum of its int8 values.
