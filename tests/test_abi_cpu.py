@@ -103,6 +103,19 @@ def test_argument_checks_come_before_the_device():
     assert L.w4a8_chain_plan_wait(None, 0) == -1
     assert L.w4a8_chain_plan_destroy(None) == 0
     assert kv260gemv.strerror(-7).startswith("a bounded wait")
+    # gate|up quantizing its act: k = 2048 only, whole Q8_0 blocks per workgroup, act 16-byte aligned
+    assert L.w4a8_gemv_gate_up_silu_q8_0(fake, fake, None, 1e-5, fake, 64, 4096, None) == -2
+    assert L.w4a8_gemv_gate_up_silu_q8_0(fake, fake, None, 1e-5, fake, 16, 2048, None) == -2
+    assert L.w4a8_gemv_gate_up_silu_q8_0(fake, fake, None, 1e-5, fake + 4, 64, 2048, None) == -3
+    assert L.w4a8_gemv_gate_up_silu_q8_0(fake, fake, None, 1e-5, None, 64, 2048, None) == -1
+    # plan steps: an engine-layout x takes no rmsnorm; kinds past the last are refused
+    S = kv260gemv.PlanStep
+    one = (S * 1)(S(kv260gemv.PLAN_GEMV_ENGINE, fake, fake, fake, 64, 2048, fake, 1e-5))
+    assert L.w4a8_chain_plan_create_steps(ctypes.cast(one, ctypes.c_void_p), 1, ctypes.byref(plan)) == -2
+    one = (S * 1)(S(5, fake, fake, fake, 64, 2048, None, 0.0))
+    assert L.w4a8_chain_plan_create_steps(ctypes.cast(one, ctypes.c_void_p), 1, ctypes.byref(plan)) == -2
+    one = (S * 1)(S(kv260gemv.PLAN_GATE_UP_SILU_Q8, fake, fake, fake, 64, 4096, None, 0.0))
+    assert L.w4a8_chain_plan_create_steps(ctypes.cast(one, ctypes.c_void_p), 1, ctypes.byref(plan)) == -2
 
 
 class Udmabuf(ctypes.Structure):
