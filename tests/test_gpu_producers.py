@@ -52,7 +52,8 @@ def test_silu_mul_q8_0(gpu, k, m):
     assert_bytes_equal(got, want, "silu_mul_q8_0")
 
 
-@pytest.mark.parametrize("rows,k", [(3072, 2048), (100, 256), (512, 8192), (16384, 2048), (40, 768)])
+@pytest.mark.parametrize("rows,k", [(3072, 2048), (100, 256), (512, 8192), (16384, 2048), (40, 768), (1024, 4096),
+                                    (64, 2048), (136, 2048)])
 def test_gemv_rmsnorm(gpu, rows, k):
     blocks = C.quantize_q4_0(O.normal_f32((rows, k), 70 + rows, 0.02))
     rng = np.random.default_rng(rows)
