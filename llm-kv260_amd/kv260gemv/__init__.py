@@ -151,6 +151,7 @@ def lib() -> ctypes.CDLL:
 
 
 PLAN_GEMV, PLAN_GATE_UP_SILU, PLAN_ARGMAX, PLAN_GATE_UP_SILU_Q8, PLAN_GEMV_ENGINE = 0, 1, 2, 3, 4
+CHAIN_MAX_STEPS = 96           # W4A8_CHAIN_MAX_STEPS: steps per chain, batch or plan
 
 
 class PlanStep(ctypes.Structure):
