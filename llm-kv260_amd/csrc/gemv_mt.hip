@@ -47,7 +47,16 @@ struct MtParams {
     const uint8_t *x;      // m rows of the engine layout, x_stride bytes apart
     float *y;              // y[m][rows]
     int m, rows, k, C, rpw, tiles, x_stride;
+    uint32_t nb_mul, c_mul, tok_mul;   // div_mul of k / 32, C and 8 rpw
 };
+
+// n / d for 0 <= n < 2^16 and 2 <= d <= 2^16 as one high multiply by
+// m = floor(2^32 / d) + 1 (div_mul), in place of the VALU division sequence
+// the compiler emits for a run-time divisor. Exact: n m / 2^32 = n / d + n e
+// / 2^32 with 0 < e <= 1, the excess is below 2^-16 <= 1 / d, and the
+// fractional part of n / d is at most 1 - 1 / d.
+__host__ __device__ constexpr uint32_t div_mul(uint32_t d) { return (uint32_t)((1ull << 32) / d + 1); }
+__device__ __forceinline__ int small_div(int n, uint32_t mul) { return (int)__umulhi((uint32_t)n, mul); }
 
 struct MtTile {
     u32x4 p[CHUNK_PIECES];
@@ -105,7 +114,7 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
     const int tok_dwords = (int)(x_lds_bytes(nb) / 4);
 
     const int C = P.C, rpw = P.rpw;
-    const int my_r = lane / C, my_c = lane - my_r * C;
+    const int my_r = small_div(lane, P.c_mul), my_c = lane - my_r * C;
     const int colx = my_r < rpw ? my_c : 0;
 
     // 1. The activation rows' loads, before any weight tile's.
@@ -113,7 +122,7 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int i = tid + p * nthreads;
-        const int t = i / nb, b = i - t * nb;
+        const int t = small_div(i, P.nb_mul), b = i - t * nb;
         const bool live = t < P.m;
         x_load<X_ENGINE>(P.x + (size_t)(live ? t : 0) * P.x_stride, P.k, b, live, xr[p]);
     }
@@ -126,7 +135,7 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int i = tid + p * nthreads;
-            const int t = i / nb, b = i - t * nb;
+            const int t = small_div(i, P.nb_mul), b = i - t * nb;
             if (t < P.m) x_stage<X_ENGINE, true>(xr[p], b, s_x + t * tok_dwords);
         }
         __syncthreads();
@@ -188,8 +197,8 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
                                                           store ? 4 * ((t0 + u) * P.rows + row) : OUT_OF_RANGE, 0, 0);
                 }
             } else {
-                const int per_tok = 8 * rpw, tok_pass = 64 / per_tok;
-                const int sum_u = lane / per_tok, sum_r = (lane - sum_u * per_tok) >> 3;
+                const int per_tok = 8 * rpw, tok_pass = small_div(64, P.tok_mul);
+                const int sum_u = small_div(lane, P.tok_mul), sum_r = (lane - sum_u * per_tok) >> 3;
                 const int srow = tile * rpw + sum_r;
                 for (int u0 = 0; u0 < TG; u0 += tok_pass) {
                     const int u = u0 + sum_u;
@@ -250,7 +259,7 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
     const int tok_dwords = (int)(x_lds_bytes(nb) / 4);
 
     const int C = P.C, rpw = P.rpw;
-    const int my_r = lane / C, my_c = lane - my_r * C;
+    const int my_r = small_div(lane, P.c_mul), my_c = lane - my_r * C;
     const int colx = my_r < rpw ? my_c : 0;
 
     // 1. The activation rows' loads, then this wave's pieces of the tile.
@@ -258,7 +267,7 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int i = tid + p * nthreads;
-        const int t = i / nb, b = i - t * nb;
+        const int t = small_div(i, P.nb_mul), b = i - t * nb;
         const bool live = t < P.m;
         x_load<X_ENGINE>(P.x + (size_t)(live ? t : 0) * P.x_stride, P.k, b, live, xr[p]);
     }
@@ -282,7 +291,7 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int i = tid + p * nthreads;
-        const int t = i / nb, b = i - t * nb;
+        const int t = small_div(i, P.nb_mul), b = i - t * nb;
         if (t < P.m) x_stage<X_ENGINE, true>(xr[p], b, s_x + t * tok_dwords);
     }
     {
@@ -322,8 +331,8 @@ __device__ void gemv_mt_split_body(const MtParams &P, int block, uint8_t *lds) {
     const int acc_a = lane & 7;
     const __amdgpu_buffer_rsrc_t y_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(P.y, 0, 4 * P.rows * P.m, BUFFER_DWORD3);
-    const int per_tok = 8 * rpw, tok_pass = 64 / per_tok;
-    const int sum_u = lane / per_tok, sum_r = (lane - sum_u * per_tok) >> 3;
+    const int per_tok = 8 * rpw, tok_pass = small_div(64, P.tok_mul);
+    const int sum_u = small_div(lane, P.tok_mul), sum_r = (lane - sum_u * per_tok) >> 3;
     const int srow = tile * rpw + sum_r;
     for (int u0 = 0; u0 < TG; u0 += tok_pass) {
         const int u = u0 + sum_u;
@@ -419,6 +428,9 @@ hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, i
     P.C = k / 256;
     P.rpw = 64 / P.C;
     P.tiles = (rows + P.rpw - 1) / P.rpw;
+    P.nb_mul = div_mul((uint32_t)(k / QK));
+    P.c_mul = div_mul((uint32_t)P.C);
+    P.tok_mul = div_mul((uint32_t)(8 * P.rpw));
     P.x_stride = k + k / 8;
     const int nb = k / QK;
     const int cus = device_cu_count();
