@@ -279,8 +279,8 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     // (l / 2) % C of row 2 (l / 2C) + l % 2 of the tile.
     const bool paired = !PLAIN && P.paired;
     const int pq = paired ? lane >> 1 : lane;
-    const int my_c = pq - (pq / C) * C;
-    const bool lane_live = paired ? lane < 2 * P.prw * C : lane / C < rpw;
+    const int my_c = pq - lane_quot(pq, C) * C;
+    const bool lane_live = paired ? lane < 2 * P.prw * C : lane_quot(lane, C) < rpw;
     // Rows per tile as the ordered sums see them.
     const int trows = paired ? 2 * P.prw : rpw;
 
@@ -289,7 +289,8 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     const bool up_wave = PAIR && wave >= pv;
     int tile = PAIR ? (up_wave ? (P.tiles >> 1) + block * pv + wave - pv : block * pv + wave) : block * waves + wave;
     const int tstride = PAIR ? P.tiles : nblocks * waves;
-    const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
+    // Tiles of this wave; the division only where a wave has two or more.
+    const int n_my = tile >= P.tiles ? 0 : tile + tstride >= P.tiles ? 1 : (P.tiles - 1 - tile) / tstride + 1;
 
     // 1. The activation. Its loads go out before any weight tile's; the
     // staging below waits for them only.

@@ -21,6 +21,16 @@ constexpr uint32_t BUFFER_DWORD3 = 0x00020000;   // raw dword access on gfx9-fam
 constexpr int CACHE_NT = 2;                       // non-temporal (streamed once)
 constexpr int SC1 = 16;                           // device-scope coherent access (sc1)
 
+// n / d for 0 <= n < 64 and 1 <= d <= 64 (a lane's row in its tile) as
+// floor((n + 0.5) * rcp(d)), four VALU operations in place of the division
+// sequence the compiler emits for a run-time divisor. Exact: n + 0.5 lies at
+// least 0.5 from a multiple of d, a margin of 0.5 / 64 in the quotient, far
+// above v_rcp_f32's one-ulp error (checked for every n, d and rcp result
+// within one ulp).
+__device__ __forceinline__ int lane_quot(int n, int d) {
+    return (int)(((float)n + 0.5f) * __builtin_amdgcn_rcpf((float)d));
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, BUFFER_DWORD3);
 }
