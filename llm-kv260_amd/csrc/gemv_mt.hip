@@ -129,7 +129,8 @@ __device__ void gemv_mt_body(const MtParams &P, int block, int nblocks, uint8_t 
 
     int tile = block * waves + wave;
     const int tstride = nblocks * waves;
-    const int n_my = tile < P.tiles ? (P.tiles - 1 - tile) / tstride + 1 : 0;
+    // Tiles of this wave; the division only where a wave has two or more.
+    const int n_my = tile >= P.tiles ? 0 : tile + tstride >= P.tiles ? 1 : (P.tiles - 1 - tile) / tstride + 1;
 
     auto stage_x = [&]() {
 #pragma unroll
