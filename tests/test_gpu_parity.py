@@ -252,6 +252,9 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       (2, 1, 4096), (2, 300, 6144), (3, 8200, 2048), (4, 8197, 2048),
                                       (4, 2048, 8192), (3, 1000, 8192), (2, 5, 8192), (5, 2048, 8192),
                                       (6, 777, 8192), (5, 3, 8192),
+                                      # k = 2304: 9 chunks and 72 blocks a row, 7 rows a tile (odd
+                                      # divisors in the kernel's lane and staging quotients), both forms
+                                      (2, 300, 2304), (2, 7, 2304), (4, 8200, 2304),
                                       # 8-row items (K >= 8192, fewer 16-row groups than CUs): the
                                       # down shape, ragged rows, one item, several token groups
                                       (8, 2048, 8192), (5, 1003, 8192), (16, 8, 8192), (12, 2050, 8192),
