@@ -391,9 +391,15 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
 
     const int acc_r = lane >> 3, acc_a = lane & 7;
     unsigned long long best = 0;          // argmax epilogue: this lane's best key
-    const __amdgpu_buffer_rsrc_t y_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(P.y, 0, PAIR == PAIR_Q8 ? P.rows / 2 + P.rows / 16 : 4 * (PAIR ? P.rows / 2 : P.rows),
-                                          BUFFER_DWORD3);
+    // y's buffer resource is made where y is stored, not here: P.y is not
+    // among the preloaded arguments, and a resource made up front has the
+    // wave wait for its argument fetch before the weight loads go out.
+    auto y_rsrc_of = [&]() {
+        return __builtin_amdgcn_make_buffer_rsrc(P.y, 0,
+                                                 PAIR == PAIR_Q8 ? P.rows / 2 + P.rows / 16
+                                                                 : 4 * (PAIR ? P.rows / 2 : P.rows),
+                                                 BUFFER_DWORD3);
+    };
     // One tile: buffer -> slab (load order) -> chunk (lane order) -> terms ->
     // slab -> ordered lane sums -> tree -> y; with REFILL the buffer then
     // receives the tile DEPTH strides ahead while the terms are computed.
@@ -443,7 +449,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                     const float gate = reinterpret_cast<const float *>(lds + (size_t)(wave - pv) * TILE_BYTES)[acc_r < rpw ? acc_r : 0];
                     const int row = (tile - (P.tiles >> 1)) * rpw + acc_r;
                     const float act = silu_mul(gate, yv);
-                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, mine && row < (P.rows >> 1) ? 4 * row : OUT_OF_RANGE, act);
+                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc_of(), mine && row < (P.rows >> 1) ? 4 * row : OUT_OF_RANGE, act);
                 }
             } else {
                 // The block's 32 act values go to the first floats of the
@@ -471,8 +477,8 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                                           ((uint32_t)(uint8_t)q8_round(v.z, inv) << 16) |
                                           ((uint32_t)(uint8_t)q8_round(v.w, inv) << 24);
                     const int n = P.rows >> 1;
-                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, 32 * block + 4 * lane, __uint_as_float(word));
-                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, lane == 0 ? n + 4 * block : OUT_OF_RANGE,
+                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc_of(), 32 * block + 4 * lane, __uint_as_float(word));
+                    store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc_of(), lane == 0 ? n + 4 * block : OUT_OF_RANGE,
                                                      half_bits_to_float(float_to_half_bits(d)));
                 }
             }
@@ -480,7 +486,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
             const float yv = tree8_dpp(lane_sum(acc_r));
             const int row = row_of(acc_r);
             const bool mine = acc_a == 0 && row >= 0;
-            store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc, mine ? 4 * row : OUT_OF_RANGE, yv);
+            store_y<(COH & COH_Y) ? SC1 : 0>(y_rsrc_of(), mine ? 4 * row : OUT_OF_RANGE, yv);
             if constexpr (ARGMAX) {
                 if (mine) best = max_u64(best, argmax_key(yv, row));
             }
