@@ -27,9 +27,11 @@ Prints one JSON line. Besides the chain (value), it reports:
                step): average algorithmic bytes per launch / average launch
                duration, both over the timed region (the host clock around the
                plan's launch and wait, dispatch boundaries included); beside
-               it, kernel_durations: the same bytes over the sum of the 65
-               kernels' average durations in the committed rocprofv3 trace of
-               `bench.py --chain-only`
+               it, kernel_durations: the same bytes over the dispatches' own
+               spans, stamped inside the kernels by a timed launch of the same
+               plan in the same run (w4a8_chain_plan_launch_timed: first wave
+               start to last wave end of each dispatch, on the device's
+               constant-rate clock), per shape and summed per step
   chain_graph  the chain through w4a8_chain_gemv in a HIP graph (HIP events
                on the launch stream around the replays), verified the same way
   chain_one_launch  the chain as one cooperative launch per step
@@ -547,20 +549,85 @@ def run_call_costs():
     return out
 
 
-KERNEL_SUMMARY = os.path.join("profiles", "gemv_kernels_llama1b_chain_only.txt")
 
 
-def kernel_durations():
-    """The chain's per-step sum of kernel durations from the committed rocprofv3
-    kernel trace of `bench.py --chain-only` (its JSON line), or None."""
-    try:
-        with open(os.path.join(ROOT, KERNEL_SUMMARY)) as f:
-            for line in f:
-                if line.startswith("JSON "):
-                    return json.loads(line[5:])
-    except OSError:
-        pass
-    return None
+def dispatch_spans(st, grid, passes):
+    """Per-workgroup stamps (uint64 [slots, 2]: start, end) of a timed launch ->
+    per-dispatch [passes * n, 2]: the earliest start and the latest end of its
+    workgroups (w4a8_chain_plan_launch_timed's layout: dispatch after dispatch,
+    grid[j] workgroups for step j)."""
+    import numpy as np
+    counts = np.tile(np.asarray(grid, dtype=np.int64), passes)
+    first = np.concatenate(([0], np.cumsum(counts)[:-1]))
+    t = st.astype(np.int64)
+    return np.stack([np.minimum.reduceat(t[:, 0], first), np.maximum.reduceat(t[:, 1], first)], axis=1)
+
+
+def stamp_stats(t, hz, chain, ms_per_step, dt_timed):
+    """The timed launch's dispatch spans: t is int64 [passes * n, 2] (first wave
+    start, last wave end) in ticks of hz. Per shape: the mean, median, min and
+    max span; per step: the spans' sum, and the gaps between one dispatch's last
+    wave end and the next one's first wave start (the dispatch boundary)."""
+    import numpy as np
+    n = len(chain)
+    us = (t[:, 1] - t[:, 0]).astype(np.float64) / hz * 1e6
+    passes = len(us) // n
+    spans = us.reshape(passes, n)
+    gaps = (t[1:, 0] - t[:-1, 1]).astype(np.float64) / hz * 1e6
+    shapes = {}
+    for j, m in enumerate(chain):
+        key = m.name.split(".")[-1]
+        shapes.setdefault(key, {"rows": m.rows, "k": m.k, "bytes": m.algorithmic_bytes, "cols": []})["cols"].append(j)
+    per_shape = {}
+    for key, d in shapes.items():
+        v = spans[:, d["cols"]].reshape(-1)
+        per_shape[key] = {"shape": f"{d['rows']}x{d['k']}", "dispatches": int(v.size),
+                          "mean_us": round(float(v.mean()), 3), "median_us": round(float(np.median(v)), 3),
+                          "min_us": round(float(v.min()), 3), "max_us": round(float(v.max()), 3),
+                          "gbps_at_mean": round(d["bytes"] / (float(v.mean()) * 1e-6) / 1e9, 1)}
+    step_sum = spans.sum(axis=1)
+    first_to_last = (t[n - 1::n, 1] - t[0::n, 0]).astype(np.float64) / hz * 1e6
+    chain_bytes = sum(m.algorithmic_bytes for m in chain)
+    ks = float(step_sum.mean())
+    return {
+        "source": "in-kernel stamps: w4a8_chain_plan_launch_timed, the same plan and kernels (their timed twins), "
+                  f"{passes} passes in one launch, this run",
+        "clock_hz": int(hz), "passes": passes,
+        "sum_us_per_step": round(ks, 2), "median_sum_us_per_step": round(float(np.median(step_sum)), 2),
+        "achieved": round(chain_bytes / (ks * 1e-6) / 1e9, 1),
+        "frac": round(chain_bytes / (ks * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "gap_us_mean": round(float(gaps.mean()), 3), "gap_us_median": round(float(np.median(gaps)), 3),
+        "first_start_to_last_end_us_per_step": round(float(first_to_last.mean()), 2),
+        "timed_launch_us_per_step": round(dt_timed * 1e6 / passes, 2),
+        "untimed_us_per_step": round(ms_per_step * 1e3, 2),
+        "per_shape": per_shape,
+        "note": "kernel time only: each dispatch from its first workgroup's start to its last workgroup's end "
+                "(every wave done, its stores landed); the boundaries between dispatches are the gaps",
+    }
+
+
+def write_stamp_summary(path, kd, argv):
+    """The timed launch's per-shape spans as a short text summary (profiles/)."""
+    lines = ["# Chain plan dispatch spans, stamped inside the kernels (w4a8_chain_plan_launch_timed)",
+             f"# command: python bench.py {' '.join(argv)}",
+             f"# {kd['passes']} passes x 65 dispatches; clock {kd['clock_hz']} Hz (s_memrealtime)",
+             "",
+             f"{'shape':10s} {'rows x k':>12s} {'n':>6s} {'mean us':>9s} {'median':>9s} {'min':>8s} {'max':>8s} "
+             f"{'GB/s@mean':>10s}"]
+    for key, r in kd["per_shape"].items():
+        lines.append(f"{key:10s} {r['shape']:>12s} {r['dispatches']:6d} {r['mean_us']:9.3f} {r['median_us']:9.3f} "
+                     f"{r['min_us']:8.3f} {r['max_us']:8.3f} {r['gbps_at_mean']:10.1f}")
+    lines += ["",
+              f"sum of the 65 spans per step: {kd['sum_us_per_step']} us (median {kd['median_sum_us_per_step']}), "
+              f"{kd['achieved']} GB/s, frac {kd['frac']}",
+              f"boundary (last wave end -> next first wave start): mean {kd['gap_us_mean']} us, "
+              f"median {kd['gap_us_median']} us",
+              f"first start -> last end per step: {kd['first_start_to_last_end_us_per_step']} us; "
+              f"timed launch {kd['timed_launch_us_per_step']} us/step (host clock); "
+              f"untimed launch {kd['untimed_us_per_step']} us/step",
+              "JSON " + json.dumps({k: v for k, v in kd.items() if k != "note"})]
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
 
 
 def cpu_baseline(chain, mats, xs, budget_s=30.0):
@@ -603,20 +670,11 @@ def cpu_baseline(chain, mats, xs, budget_s=30.0):
 
 
 def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph):
-    plan = not args.no_plan
     """The fields every bench line carries: the metric, the chain and its roofline."""
+    plan = not args.no_plan
     n = len(cf.decode_chain())
     chain_bytes = cf.chain_algorithmic_bytes()
-    kernel = None
-    if kd.get("per_step_sum_us"):
-        ks = kd["per_step_sum_us"]
-        kernel = {"source": KERNEL_SUMMARY, "sum_us_per_step": ks,
-                  "achieved": round(chain_bytes / (ks * 1e-6) / 1e9, 1),
-                  "frac": round(chain_bytes / (ks * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                  "profiled_run_us_per_step": kd.get("profiled_us_per_step"),
-                  "note": "the sum of the 65 kernels' average durations (rocprofv3 kernel trace of "
-                          "bench.py --chain-only): the time the chain's kernels run, without the launch "
-                          "boundaries between them"}
+    kernel = kd or None
     return {
         "metric": "1B-shape decode GEMV-chain tokens/s (W4A8 Q4_0 x Q8_0, 65 GEMVs per token)",
         "value": round(1e3 / ms_per_step, 2),
@@ -637,7 +695,8 @@ def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd
                                "activation re-quantized to Q8_0 before every matrix, matrices in order",
                    "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
                    "algorithmic_bytes_per_step": chain_bytes},
-        "verified": (chain_check["ok"] and chain_check["weights_ok"] and graph["verified"] and
+        "verified": (chain_check["ok"] and chain_check["weights_ok"] and chain_check.get("timed_launch_ok", True) and
+                     graph["verified"] and
                      (one_launch is None or one_launch["verified"])),
         "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
@@ -670,12 +729,18 @@ def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, w
     return out
 
 
-def time_plan(torch, kv, L, ptr, n, steps, warmup, ys):
+def time_plan(torch, kv, L, ptr, n, steps, warmup, ys, check, stamp_passes):
     """ms per step of the chain plan: `warmup` passes, then exactly `steps`
     passes in one launch, waited for; the device is idle (synchronized) on
-    both sides of the timed region and the outputs are poisoned before it."""
+    both sides of the timed region and the outputs are poisoned before it;
+    check() verifies them. Then, outside the timed region, `stamp_passes`
+    passes of the same plan as a timed launch (its outputs poisoned and
+    verified the same way): the raw stamps, their clock and the launch's host
+    time."""
+    import numpy as np
     plan = ctypes.c_void_p()
     kv.check("w4a8_chain_plan_create", L.w4a8_chain_plan_create(ptr, n, ctypes.byref(plan)))
+    stamps = None
     try:
         kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, max(warmup, 1)))
         kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
@@ -686,9 +751,28 @@ def time_plan(torch, kv, L, ptr, n, steps, warmup, ys):
         kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 120000))
         dt = time.perf_counter() - t0
         torch.cuda.synchronize()
+        result = check()
+        if stamp_passes:
+            grid = [L.w4a8_chain_plan_workgroups(plan, j) for j in range(n)]
+            buf = torch.zeros(2 * stamp_passes * sum(grid), dtype=torch.int64, device="cuda")
+            poison(ys)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            kv.check("w4a8_chain_plan_launch_timed", L.w4a8_chain_plan_launch_timed(plan, stamp_passes,
+                                                                                   buf.data_ptr()))
+            kv.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 120000))
+            dt_timed = time.perf_counter() - t1
+            torch.cuda.synchronize()
+            timed_check = check()
+            hz = ctypes.c_int64()
+            kv.check("w4a8_wall_clock_hz", L.w4a8_wall_clock_hz(ctypes.byref(hz)))
+            per_wg = buf.cpu().numpy().view(np.uint64).reshape(-1, 2)
+            if (per_wg == 0).any():
+                raise RuntimeError("a workgroup of the timed launch left its stamp slot unwritten")
+            stamps = (dispatch_spans(per_wg, grid, stamp_passes), hz.value, dt_timed, timed_check)
     finally:
         kv.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
-    return dt * 1e3 / steps, dt
+    return dt * 1e3 / steps, dt, result, stamps
 
 
 def main() -> int:
@@ -708,6 +792,10 @@ def main() -> int:
     ap.add_argument("--no-plan", action="store_true",
                     help="time the chain through w4a8_chain_gemv only (the headline then comes from the HIP "
                          "graph)")
+    ap.add_argument("--stamp-passes", type=int, default=100,
+                    help="passes of the plan's timed launch (in-kernel dispatch spans; 0 = none)")
+    ap.add_argument("--stamp-summary", default=None, metavar="PATH",
+                    help="write the timed launch's per-shape dispatch spans to PATH as a text summary")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first copy MB of device memory once: a plain copy of known size whose "
                          "FETCH_SIZE / WRITE_SIZE counters scale the kernels' HBM traffic")
@@ -740,13 +828,23 @@ def main() -> int:
     ptr = ctypes.cast(steps, ctypes.c_void_p)
     chain_digests = [(r["name"], y, r["y"]) for y, r in zip(ys, recs)]
 
+    kd = {}
     if not args.no_plan:
         log(f"timing {args.steps} steps after {args.warmup} warm-up steps (chain plan)")
-        ms_per_step, wall = time_plan(torch, kv, L, ptr, n, args.steps, args.warmup, ys)
-        chain_check = verify(chain_digests)
+        ms_per_step, wall, chain_check, stamps = time_plan(torch, kv, L, ptr, n, args.steps, args.warmup, ys,
+                                                           lambda: verify(chain_digests), args.stamp_passes)
         chain_check["weights_ok"] = weights_ok
         log(f"chain (plan): {ms_per_step * 1e3:.1f} us/step, {1e3 / ms_per_step:.0f} tokens/s, "
             f"outputs {'match' if chain_check['ok'] else 'DIFFER FROM'} the oracle's digests")
+        if stamps is not None:
+            st, hz, dt_timed, timed_check = stamps
+            kd = stamp_stats(st, hz, chain, ms_per_step, dt_timed)
+            kd["verified"] = timed_check["ok"]
+            chain_check["timed_launch_ok"] = timed_check["ok"]
+            log(f"chain (plan, timed launch): dispatch spans sum to {kd['sum_us_per_step']} us/step "
+                f"(frac {kd['frac']}), boundary median {kd['gap_us_median']} us, verified {timed_check['ok']}")
+            if args.stamp_summary:
+                write_stamp_summary(args.stamp_summary, kd, sys.argv[1:])
 
     log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay of w4a8_chain_gemv)")
     g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
@@ -797,7 +895,6 @@ def main() -> int:
         for r in prefill:
             log(f"prefill {r['tokens']} tokens: {r['ms_per_prompt']} ms, {r['tokens_per_s']} tokens/s "
                 f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token), verified {r['verified']}")
-    kd = kernel_durations() or {}
     if args.chain_only:
         out = chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph)
         print(json.dumps(out), flush=True)
@@ -860,7 +957,8 @@ def main() -> int:
     if not args.no_cpu:
         log("CPU baseline (bounded sample)")
         cpu = cpu_baseline(chain, mats, xs)
-    verified = (chain_check["ok"] and weights_ok and batch_check["ok"] and graph["verified"] and
+    verified = (chain_check["ok"] and weights_ok and chain_check.get("timed_launch_ok", True) and
+                batch_check["ok"] and graph["verified"] and
                 fused_chain.get("plan", {}).get("verified", True) and
                 fused_chain["fp32_act"].get("plan", {}).get("verified", True) and
                 (one_launch is None or one_launch["verified"]) and

@@ -111,7 +111,11 @@ int w4a8_topk(const float *y, int n, int k, float *vals, int32_t *idx, void *wor
  * 1 <= n <= W4A8_TOPK_NO_ALLOC_MAX_N (larger n: W4A8_ERR_SHAPE), 1 <= k <= 64.
  * The array belongs to the device current at the call; every call on that
  * device shares it, so calls that overlap on one device (two streams, two
- * threads) race and may return wrong candidates: serialize them. */
+ * threads) race and may return wrong candidates: serialize them (replays of
+ * a graph that captured the call share it too). The call may be captured
+ * into a HIP graph, the first call on a device included: that call looks up
+ * the array's address with this thread's capture mode relaxed for the
+ * lookup. */
 #define W4A8_TOPK_NO_ALLOC_MAX_N 262144
 int w4a8_topk_no_alloc(const float *y, int n, int k, float *vals, int32_t *idx, void *stream);
 
@@ -209,7 +213,9 @@ typedef struct w4a8_chain_step {
  * Step j reads its activation only after every row of step j-1's output is
  * written, so x_j may be (or be computed from) an earlier y; each step
  * equals w4a8_gemv_f32 on its own, byte for byte. 1 <= n <=
- * W4A8_CHAIN_MAX_STEPS.
+ * W4A8_CHAIN_MAX_STEPS. A step whose y overlaps its own x or weights is
+ * refused (W4A8_ERR_SHAPE): its workgroups would race. Steps may share
+ * output bytes; the later step's win.
  *
  * By default (W4A8_CHAIN_PER_STEP) each step is one kernel, in stream order.
  * In W4A8_CHAIN_ONE_LAUNCH mode, a chain whose every k is in 2048..8192 is
@@ -267,7 +273,17 @@ int w4a8_chain_timeouts(void);
  *     timeout_ms (W4A8_ERR_TIMEOUT); after W4A8_OK the outputs are visible
  *     to the host and to any later HIP work;
  *   - destroy: waits (at most 10 s) and frees the plan.
- * Launches of plans on one device go to that device's queue in call order. */
+ * Launches of plans on one device go to that device's queue in call order.
+ * A launch that finds the queue full waits for the device to take packets;
+ * if the device takes none for 10 s it is stalled: the launch returns
+ * W4A8_ERR_TIMEOUT, the plan's wait and destroy keep reporting the timeout
+ * (its argument blocks stay allocated, since queued packets point at them),
+ * and every later launch on that device fails at once.
+ * Outputs: a step's y may be another step's x (in the same pass or the
+ * next) and may share bytes with other steps' y (the later step's bytes
+ * win, as in a stream); create refuses (W4A8_ERR_SHAPE) a step whose x
+ * overlaps its own y, and any step's weights, norm_w, argmax or workspace
+ * that overlap a step's y. */
 typedef struct w4a8_chain_plan w4a8_chain_plan;
 int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan);
 
@@ -289,9 +305,10 @@ int w4a8_chain_plan_create(const w4a8_chain_step *steps, int n, w4a8_chain_plan 
  *                             (int8[k] | float32[k / 32]), norm_w NULL --
  *                             down after W4A8_PLAN_GATE_UP_SILU_Q8.
  * Every k in 2048..W4A8_MAX_K; the rest as w4a8_chain_plan_create (which is
- * this with every step a W4A8_PLAN_GEMV without norm_w). A step may read an
- * earlier (or, over passes, a later) step's y; norm_w, argmax and the
- * workspace must not be another step's y. */
+ * this with every step a W4A8_PLAN_GEMV without norm_w), with the same
+ * rules for outputs: a step may read an earlier (or, over passes, a later)
+ * step's y; weights, norm_w, argmax and the workspace must not overlap any
+ * step's y (W4A8_ERR_SHAPE). */
 #define W4A8_PLAN_GEMV 0
 #define W4A8_PLAN_GATE_UP_SILU 1
 #define W4A8_PLAN_ARGMAX 2
@@ -314,13 +331,38 @@ int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes);
 int w4a8_chain_plan_wait(w4a8_chain_plan *plan, int timeout_ms);
 int w4a8_chain_plan_destroy(w4a8_chain_plan *plan);
 
+/* A launch of the plan that also times each dispatch, from inside the
+ * kernels (no tool intercepts the queue): the same kernels with the same
+ * outputs, each workgroup reading the device's constant-rate clock when its
+ * first wave starts and when all its waves are done (their stores landed),
+ * and storing the two readings in a slot of its own (no atomics). Dispatch
+ * i of the launch (pass i / n, step j = i % n) has
+ * w4a8_chain_plan_workgroups(plan, j) workgroups; workgroup g of it writes
+ * stamps[2 s] (start) and stamps[2 s + 1] (end), s = g plus the workgroup
+ * counts of the dispatches before i. A dispatch's span is the latest end
+ * minus the earliest start of its workgroups, in ticks of
+ * w4a8_wall_clock_hz. stamps: device memory, 16-byte aligned, 2 * passes *
+ * w4a8_chain_plan_workgroups(plan, -1) words; passes times that count at
+ * most W4A8_PLAN_TIMED_MAX_SLOTS. The call waits for the plan's earlier
+ * launches first (it rewrites the timed argument blocks), and the stamps are
+ * valid once w4a8_chain_plan_wait returns W4A8_OK. A measurement aid: the
+ * plain launch stays the one to use. */
+#define W4A8_PLAN_TIMED_MAX_SLOTS (1L << 22)
+int w4a8_chain_plan_launch_timed(w4a8_chain_plan *plan, int passes, uint64_t *stamps);
+/* Workgroups of step `step` of the plan's dispatches (step -1: the sum over
+ * all steps, one pass), or a negative status. */
+long w4a8_chain_plan_workgroups(const w4a8_chain_plan *plan, int step);
+/* Ticks per second of the clock the timed launch stamps with (current device). */
+int w4a8_wall_clock_hz(int64_t *hz);
+
 /* The same n GEMVs with no order between them, in one launch: every matrix
  * streams at once, so small matrices no longer pay a launch and a latency
  * tail each. Each y equals w4a8_gemv_f32 on its own, byte for byte. For
  * matrices that share an activation or are consumed together -- the
  * reference fuses q|k|v and gate|up into single matrices for this reason
  * (board/tp/tp_llama.cpp:258-268) -- or for a batch of independent
- * requests. Outputs must not overlap inputs. 1 <= n <= W4A8_CHAIN_MAX_STEPS. */
+ * requests. No output may overlap any entry's x or weights, or another
+ * entry's output (W4A8_ERR_SHAPE). 1 <= n <= W4A8_CHAIN_MAX_STEPS. */
 int w4a8_gemv_batch(const w4a8_chain_step *steps, int n, void *stream);
 
 #ifdef __cplusplus

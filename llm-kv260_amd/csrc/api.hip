@@ -31,6 +31,18 @@ int check_gemv(const void *w, const void *x, const float *y, int rows, int k, ui
     return W4A8_OK;
 }
 
+bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+    return pa < pb + nb && pb < pa + na;
+}
+
+// A GEMV whose y overlaps its own x (or weights) races: its workgroups read x
+// while others already write y.
+bool step_in_place(const w4a8_chain_step &s) {
+    const size_t wb = (size_t)s.rows * (size_t)(s.k / 32) * 18;
+    return overlaps(s.x, 4 * (size_t)s.k, s.y, 4 * (size_t)s.rows) || overlaps(s.w, wb, s.y, 4 * (size_t)s.rows);
+}
+
 MatrixRef plain_matrix(const void *w, int rows, int k) {
     MatrixRef m{};
     m.seg[0] = static_cast<const uint8_t *>(w);
@@ -231,8 +243,10 @@ int w4a8_gemm(const void *w, const void *x_rows, float *y, int m, int rows, int 
 int w4a8_chain_gemv(const w4a8_chain_step *steps, int n, void *stream) {
     if (!steps) return W4A8_ERR_NULL;
     if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
-    for (int i = 0; i < n; ++i)
+    for (int i = 0; i < n; ++i) {
         if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
+        if (step_in_place(steps[i])) return W4A8_ERR_SHAPE;
+    }
     return hip_status(launch_chain(steps, n, (hipStream_t)stream));
 }
 
@@ -259,6 +273,7 @@ int w4a8_chain_plan_create_steps(const w4a8_plan_step *steps, int n, w4a8_chain_
             if (!aligned(s.argmax, 4) || !aligned(s.workspace, 16)) return W4A8_ERR_ALIGN;
         }
     }
+    if (int st = plan_check_ranges(steps, n)) return st;
     hipError_t he = hipSuccess;
     const int st = chain_plan_create(steps, n, plan, he);
     return st == W4A8_ERR_HIP ? hip_status(he) : st;
@@ -279,6 +294,33 @@ int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes) {
     if (!plan) return W4A8_ERR_NULL;
     if (passes < 1 || passes > (1 << 20)) return W4A8_ERR_SHAPE;
     return chain_plan_launch(plan, passes);
+}
+
+long w4a8_chain_plan_workgroups(const w4a8_chain_plan *plan, int step) {
+    if (!plan) return W4A8_ERR_NULL;
+    if (step < -1 || step >= chain_plan_steps(plan)) return W4A8_ERR_SHAPE;
+    return chain_plan_workgroups(plan, step);
+}
+
+int w4a8_chain_plan_launch_timed(w4a8_chain_plan *plan, int passes, uint64_t *stamps) {
+    if (!plan || !stamps) return W4A8_ERR_NULL;
+    if (passes < 1 || (long long)passes * chain_plan_workgroups(plan, -1) > W4A8_PLAN_TIMED_MAX_SLOTS)
+        return W4A8_ERR_SHAPE;
+    if (!aligned(stamps, 16)) return W4A8_ERR_ALIGN;
+    hipError_t he = hipSuccess;
+    const int st = chain_plan_launch_timed(plan, passes, reinterpret_cast<unsigned long long *>(stamps), he);
+    return st == W4A8_ERR_HIP ? hip_status(he) : st;
+}
+
+int w4a8_wall_clock_hz(int64_t *hz) {
+    if (!hz) return W4A8_ERR_NULL;
+    *hz = 0;
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return W4A8_ERR_NODEV;
+    if (int s = hip_status(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev))) return s;
+    if (khz <= 0) return W4A8_ERR_NODEV;
+    *hz = (int64_t)khz * 1000;
+    return W4A8_OK;
 }
 
 int w4a8_chain_plan_wait(w4a8_chain_plan *plan, int timeout_ms) {
@@ -313,6 +355,17 @@ int w4a8_gemv_batch(const w4a8_chain_step *steps, int n, void *stream) {
     if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
     for (int i = 0; i < n; ++i)
         if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
+    // Every entry runs at once: no output may overlap any entry's input or
+    // another entry's output.
+    for (int i = 0; i < n; ++i)
+        for (int j = 0; j < n; ++j) {
+            const w4a8_chain_step &a = steps[i], &b = steps[j];
+            const size_t ya = 4 * (size_t)a.rows;
+            const size_t wb = (size_t)b.rows * (size_t)(b.k / 32) * 18;
+            if (overlaps(a.y, ya, b.x, 4 * (size_t)b.k) || overlaps(a.y, ya, b.w, wb) ||
+                (i != j && overlaps(a.y, ya, b.y, 4 * (size_t)b.rows)))
+                return W4A8_ERR_SHAPE;
+        }
     return hip_status(launch_gemv_batch(steps, n, (hipStream_t)stream));
 }
 

@@ -644,13 +644,22 @@ hipError_t launch_chain_one(const w4a8_chain_step *steps, int n, hipStream_t str
         A.s[i] = ChainStep{static_cast<const uint8_t *>(steps[i].w), steps[i].x, steps[i].y, (uint32_t)steps[i].rows,
                            pack_geo(C, rpw, tiles % grid, tiles / grid)};
     }
-    // Which outputs feed a later step's activation within this launch.
+    // Which outputs feed a later step's activation within this launch; and
+    // outputs that share bytes with another step's output, which are written
+    // through as well: the two steps map those rows to different workgroups,
+    // and so to different XCDs' L2s, whose dirty copies the launch's closing
+    // release would write back in no defined order.
     for (int j = 0; j < n; ++j)
-        for (int i = 0; i < j; ++i)
+        for (int i = 0; i < j; ++i) {
             if (overlaps(steps[j].x, 4 * (size_t)steps[j].k, steps[i].y, 4 * (size_t)steps[i].rows)) {
                 A.s[j].rf |= X_COH;
                 A.s[i].rf |= Y_COH;
             }
+            if (overlaps(steps[j].y, 4 * (size_t)steps[j].rows, steps[i].y, 4 * (size_t)steps[i].rows)) {
+                A.s[j].rf |= Y_COH;
+                A.s[i].rf |= Y_COH;
+            }
+        }
     hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(&chain_kernel), 160 * 1024);
     if (e != hipSuccess) return e;
     int per_cu = 0;

@@ -33,6 +33,7 @@
 #include <vector>
 
 #include "gemv_m1_dev.h"
+#include "plan_ring.h"
 
 extern "C" const char w4a8_chain_plan_co_begin[];
 extern "C" const char w4a8_chain_plan_co_end[];
@@ -44,6 +45,8 @@ struct w4a8_chain_plan {
     std::vector<uint32_t> grid, threads, group;
     char *kargs = nullptr;                 // pinned host memory, ARG_STRIDE bytes per step
     hsa_signal_t done{};                   // launches in flight
+    char *timed_kargs = nullptr;           // the timed launch's, device memory: one block per dispatch
+    size_t timed_bytes = 0;
 };
 
 namespace w4a8 {
@@ -58,6 +61,9 @@ struct PlanArgs {
     GemvParams P;
 };
 static_assert(sizeof(PlanArgs) == 176, "argument block of the plan's kernels");
+// The timed twins take one more argument after the block: the dispatch's
+// two stamp words.
+constexpr size_t TIMED_ARGS_BYTES = sizeof(PlanArgs) + sizeof(unsigned long long *);
 constexpr size_t ARG_STRIDE = 256;
 constexpr uint32_t QUEUE_PACKETS = 16384;
 // Kernel variants: (kernel kind) x (x format) x (coherence), in
@@ -95,17 +101,21 @@ size_t y_bytes(const w4a8_plan_step &s) {
     if (s.kind == W4A8_PLAN_GATE_UP_SILU_Q8) return (size_t)(s.rows / 2) + (size_t)(s.rows / 16);
     return 4 * (size_t)s.rows;
 }
-constexpr double QUEUE_SPACE_WAIT_S = 10.0;    // bound on waiting for free packet slots
+// A launch waiting for free packet slots gives up once the device has taken
+// no packet for this long: the device is then stalled, not merely busy.
+constexpr double QUEUE_STALL_S = 10.0;
 
 struct DeviceRuntime {
     std::mutex m;                  // one producer on the queue at a time
     bool tried = false;
     int status = W4A8_OK;
+    bool stalled = false;          // a launch found the queue stalled: every later launch fails
     hsa_agent_t agent{};
     hsa_queue_t *queue = nullptr;
     hsa_executable_t exe{};
-    uint64_t kobj[N_KERNELS]{};
-    uint32_t group[N_KERNELS]{}, priv[N_KERNELS]{};
+    // [0]: the kernels, [1]: their timed twins.
+    uint64_t kobj[2][N_KERNELS]{};
+    uint32_t group[2][N_KERNELS]{}, priv[2][N_KERNELS]{};
 };
 constexpr int MAX_DEVICES = 16;
 DeviceRuntime g_rt[MAX_DEVICES];
@@ -162,21 +172,30 @@ int runtime_of(int dev, DeviceRuntime *&out) {
         hsa_executable_load_agent_code_object(rt.exe, rt.agent, rd, nullptr, nullptr) != HSA_STATUS_SUCCESS ||
         hsa_executable_freeze(rt.exe, nullptr) != HSA_STATUS_SUCCESS)
         return rt.status;
-    for (int v = 0; v < N_KERNELS; ++v) {
-        const int kk = v / (4 * N_FORMATS), fmt = (v / 4) % N_FORMATS;
-        if (!HAS_FORMAT[kk][fmt]) continue;
-        hsa_executable_symbol_t sym;
-        char name[64];
-        std::snprintf(name, sizeof name, "w4a8_plan_%s_%s%s.kd", KIND_NAMES[kk], FORMAT_NAMES[fmt], COH_NAMES[v % 4]);
-        if (hsa_executable_get_symbol_by_name(rt.exe, name, &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
-            hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &rt.kobj[v]) !=
-                HSA_STATUS_SUCCESS ||
-            hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE, &rt.group[v]) !=
-                HSA_STATUS_SUCCESS ||
-            hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE, &rt.priv[v]) !=
-                HSA_STATUS_SUCCESS)
-            return rt.status;
-    }
+    for (int t = 0; t < 2; ++t)
+        for (int v = 0; v < N_KERNELS; ++v) {
+            const int kk = v / (4 * N_FORMATS), fmt = (v / 4) % N_FORMATS;
+            if (!HAS_FORMAT[kk][fmt]) continue;
+            hsa_executable_symbol_t sym;
+            char name[64];
+            std::snprintf(name, sizeof name, "w4a8_plan_%s_%s%s%s.kd", KIND_NAMES[kk], FORMAT_NAMES[fmt],
+                          COH_NAMES[v % 4], t ? "_t" : "");
+            uint32_t kargs = 0;
+            if (hsa_executable_get_symbol_by_name(rt.exe, name, &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &rt.kobj[t][v]) !=
+                    HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE,
+                                               &rt.group[t][v]) != HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE,
+                                               &rt.priv[t][v]) != HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_KERNARG_SEGMENT_SIZE, &kargs) !=
+                    HSA_STATUS_SUCCESS)
+                return rt.status;
+            // The argument block written per step is all a kernel may read: one
+            // that also read hidden arguments (grid sizes, code-object v5's
+            // implicit block) would find zeros there, so refuse the code object.
+            if (kargs != (t ? TIMED_ARGS_BYTES : sizeof(PlanArgs))) return rt.status;
+        }
     if (hsa_queue_create(rt.agent, QUEUE_PACKETS, HSA_QUEUE_TYPE_SINGLE, nullptr, nullptr, UINT32_MAX, UINT32_MAX,
                          &rt.queue) != HSA_STATUS_SUCCESS)
         return rt.status;
@@ -190,6 +209,30 @@ bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
 
 }  // namespace
 
+// A plan has no cache fences between its steps, so what a step writes may
+// only be read back where the plan knows to read it from the coherence point:
+// as another step's x. Everything else a step reads (its weights, norm_w) or
+// writes besides y (the argmax row and workspace) must not lie in any step's
+// y, and no step may read its own output as its x (its workgroups would race
+// with each other).
+int plan_check_ranges(const w4a8_plan_step *steps, int n) {
+    for (int i = 0; i < n; ++i) {
+        const w4a8_plan_step &s = steps[i];
+        if (overlaps(s.x, x_bytes(s), s.y, y_bytes(s))) return W4A8_ERR_SHAPE;
+        for (int j = 0; j < n; ++j) {
+            const w4a8_plan_step &o = steps[j];
+            const size_t w_bytes = (size_t)o.rows * (size_t)(o.k / QK) * Q4_0_BYTES;
+            if (overlaps(o.w, w_bytes, s.y, y_bytes(s))) return W4A8_ERR_SHAPE;
+            if (o.norm_w && overlaps(o.norm_w, 4 * (size_t)o.k, s.y, y_bytes(s))) return W4A8_ERR_SHAPE;
+            if (o.kind == W4A8_PLAN_ARGMAX &&
+                (overlaps(o.argmax, sizeof(int32_t), s.y, y_bytes(s)) ||
+                 overlaps(o.workspace, argmax_workspace_bytes(), s.y, y_bytes(s))))
+                return W4A8_ERR_SHAPE;
+        }
+    }
+    return W4A8_OK;
+}
+
 int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out, hipError_t &he) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return W4A8_ERR_NODEV;
@@ -199,14 +242,24 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
     p->device = dev;
     p->n = n;
     p->kind.assign(n, 0);
-    // Which outputs another step reads, in this pass or the next.
+    // Which outputs another step reads, in this pass or the next: written
+    // through, and read from the coherence point. Outputs that share bytes
+    // with another step's output are written through as well: each step's
+    // shape maps its rows to other workgroups, and so to other XCDs' L2s, so
+    // the shared lines could otherwise sit dirty in two L2s at once, and the
+    // launch's closing release would write both back in no defined order.
     std::vector<int> coh(n, 0);
     for (int j = 0; j < n; ++j)
-        for (int i = 0; i < n; ++i)
+        for (int i = 0; i < n; ++i) {
             if (overlaps(steps[j].x, x_bytes(steps[j]), steps[i].y, y_bytes(steps[i]))) {
                 coh[j] |= COH_X;
                 coh[i] |= COH_Y;
             }
+            if (i != j && overlaps(steps[j].y, y_bytes(steps[j]), steps[i].y, y_bytes(steps[i]))) {
+                coh[j] |= COH_Y;
+                coh[i] |= COH_Y;
+            }
+        }
     const int cus = device_cu_count();
     std::vector<PlanArgs> args(n);
     for (int j = 0; j < n; ++j) {
@@ -256,7 +309,7 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
         args[j] = a;
         p->grid.push_back((uint32_t)sh.grid);
         p->threads.push_back((uint32_t)sh.threads);
-        p->group.push_back(rt->group[p->kind[j]] + (uint32_t)sh.lds);
+        p->group.push_back((uint32_t)sh.lds);
     }
     std::vector<char> host((size_t)n * ARG_STRIDE, 0);
     for (int j = 0; j < n; ++j) std::memcpy(host.data() + (size_t)j * ARG_STRIDE, &args[j], sizeof(PlanArgs));
@@ -277,23 +330,40 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
     return W4A8_OK;
 }
 
-int chain_plan_launch(w4a8_chain_plan *p, int passes) {
+namespace {
+
+// Writes `passes` passes of the plan's dispatches to its device's queue:
+// every packet with the barrier bit (step j + 1 starts after step j ends),
+// fence scope none except an acquire at system scope on the first packet and
+// a release at system scope on the last, which carries the plan's completion
+// signal. `kargs_of(i)` is dispatch i's argument block; TIMED selects the
+// timed twins.
+template <bool TIMED, class KArgs>
+int issue(w4a8_chain_plan *p, int passes, KArgs kargs_of) {
     DeviceRuntime *rt = nullptr;
     if (const int s = runtime_of(p->device, rt)) return s;
     std::lock_guard<std::mutex> lk(rt->m);
+    if (rt->stalled) return W4A8_ERR_TIMEOUT;
     hsa_queue_t *q = rt->queue;
     const long total = (long)passes * p->n;
     hsa_signal_add_relaxed(p->done, 1);
-    uint64_t idx = 0;
-    const auto t0 = std::chrono::steady_clock::now();
-    for (long i = 0; i < total; ++i) {
+    uint64_t idx = hsa_queue_load_write_index_relaxed(q);
+    for (long i = 0; i < total; ++i, ++idx) {
         const int j = (int)(i % p->n);
-        idx = hsa_queue_add_write_index_relaxed(q, 1);
-        // A full queue: ring for what is written, then wait (bounded) for room.
-        while (idx - hsa_queue_load_read_index_scacquire(q) >= q->size) {
-            hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx - 1);
-            if (std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > QUEUE_SPACE_WAIT_S)
-                return W4A8_ERR_TIMEOUT;   // the slots taken stay unwritten: the queue is unusable after this
+        const plan_ring::Room room = plan_ring::wait_for_room(
+            idx, q->size, [q] { return hsa_queue_load_read_index_scacquire(q); },
+            [q](uint64_t last) { hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)last); },
+            QUEUE_STALL_S);
+        if (room != plan_ring::Room::OK) {
+            // The device has taken no packet for QUEUE_STALL_S: it is stalled.
+            // No slot is claimed past the packets written (the queue stays
+            // well formed), but this launch's last packet, the one carrying
+            // the completion signal, is not among them: the plan's wait and
+            // destroy report the timeout rather than free argument blocks
+            // that queued packets still point at, and every later launch on
+            // the device fails at once.
+            rt->stalled = true;
+            return W4A8_ERR_TIMEOUT;
         }
         auto *pk = reinterpret_cast<hsa_kernel_dispatch_packet_t *>(q->base_address) + (idx & (q->size - 1));
         std::memset(reinterpret_cast<char *>(pk) + 4, 0, sizeof(*pk) - 4);
@@ -304,10 +374,10 @@ int chain_plan_launch(w4a8_chain_plan *p, int passes) {
         pk->grid_size_x = p->grid[j] * p->threads[j];
         pk->grid_size_y = 1;
         pk->grid_size_z = 1;
-        pk->private_segment_size = rt->priv[v];
-        pk->group_segment_size = p->group[j];
-        pk->kernel_object = rt->kobj[v];
-        pk->kernarg_address = p->kargs + (size_t)j * ARG_STRIDE;
+        pk->private_segment_size = rt->priv[TIMED][v];
+        pk->group_segment_size = rt->group[TIMED][v] + p->group[j];
+        pk->kernel_object = rt->kobj[TIMED][v];
+        pk->kernarg_address = kargs_of(i);
         const bool first = i == 0, last = i == total - 1;
         if (last) pk->completion_signal = p->done;
         const uint16_t header =
@@ -316,15 +386,61 @@ int chain_plan_launch(w4a8_chain_plan *p, int passes) {
                        ((last ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_NONE) << HSA_PACKET_HEADER_SCRELEASE_FENCE_SCOPE));
         const uint32_t setup = 1u << HSA_KERNEL_DISPATCH_PACKET_SETUP_DIMENSIONS;
         __atomic_store_n(&pk->full_header, (uint32_t)header | (setup << 16), __ATOMIC_RELEASE);
-        // Ring once per pass, so the device starts while later passes are
-        // written, and at the ring's last slot, so that no rung range of
-        // packets wraps around the ring's end (a queue interceptor, such as a
-        // profiler's, may copy a rung range as one block: with ranges that
-        // wrapped, rocprofv3's kernel trace read past the ring and crashed).
-        if (j == p->n - 1 || ((idx + 1) & (q->size - 1)) == 0)
+        hsa_queue_store_write_index_relaxed(q, idx + 1);
+        if (plan_ring::ring_after(idx, q->size, j, p->n))
             hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
     }
     return W4A8_OK;
+}
+
+}  // namespace
+
+int chain_plan_steps(const w4a8_chain_plan *p) { return p->n; }
+
+int chain_plan_launch(w4a8_chain_plan *p, int passes) {
+    return issue<false>(p, passes, [p](long i) { return p->kargs + (size_t)(i % p->n) * ARG_STRIDE; });
+}
+
+long chain_plan_workgroups(const w4a8_chain_plan *p, int step) {
+    if (step >= 0) return step < p->n ? (long)p->grid[step] : -1;
+    long w = 0;
+    for (int j = 0; j < p->n; ++j) w += p->grid[j];
+    return w;
+}
+
+int chain_plan_launch_timed(w4a8_chain_plan *p, int passes, unsigned long long *stamps, hipError_t &he) {
+    // The argument blocks of an earlier timed launch may be rewritten below.
+    if (const int s = chain_plan_wait(p, 10000)) return s;
+    const size_t total = (size_t)passes * (size_t)p->n;
+    const size_t bytes = total * ARG_STRIDE;
+    // Every dispatch gets its own argument block (its stamp slots differ).
+    // They go to device memory: blocks the packet processor has not read
+    // before are then one device read each, as the plain launch's are.
+    if (p->timed_bytes < bytes) {
+        if (p->timed_kargs) (void)hipFree(p->timed_kargs);
+        p->timed_kargs = nullptr;
+        p->timed_bytes = 0;
+        if ((he = hipMalloc(&p->timed_kargs, bytes)) != hipSuccess) {
+            p->timed_kargs = nullptr;
+            return W4A8_ERR_HIP;
+        }
+        p->timed_bytes = bytes;
+    }
+    // Dispatch i: step i % n's argument block, then the address of its
+    // workgroups' slots (two words each, after those of the dispatches before).
+    std::vector<char> host(bytes, 0);
+    size_t slot = 0;
+    for (size_t i = 0; i < total; ++i) {
+        char *a = host.data() + i * ARG_STRIDE;
+        const size_t j = i % (size_t)p->n;
+        std::memcpy(a, p->kargs + j * ARG_STRIDE, sizeof(PlanArgs));
+        unsigned long long *st = stamps + 2 * slot;
+        std::memcpy(a + sizeof(PlanArgs), &st, sizeof st);
+        slot += p->grid[j];
+    }
+    if ((he = hipMemcpy(p->timed_kargs, host.data(), bytes, hipMemcpyHostToDevice)) != hipSuccess)
+        return W4A8_ERR_HIP;
+    return issue<true>(p, passes, [p](long i) { return p->timed_kargs + (size_t)i * ARG_STRIDE; });
 }
 
 int chain_plan_wait(w4a8_chain_plan *p, int timeout_ms) {
@@ -343,6 +459,7 @@ int chain_plan_destroy(w4a8_chain_plan *p) {
     if (s != W4A8_OK) return s;   // work in flight: the plan stays valid
     hsa_signal_destroy(p->done);
     (void)hipHostFree(p->kargs);
+    if (p->timed_kargs) (void)hipFree(p->timed_kargs);
     delete p;
     return W4A8_OK;
 }

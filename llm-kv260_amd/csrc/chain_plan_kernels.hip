@@ -29,6 +29,21 @@ __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int 
     gemv_m1_body<XF, true, true, ARGMAX, PAIR, COH>(P, blockIdx.x, nblocks, nthreads, lds);
 }
 
+// The timed twins' stamps: each workgroup's start (its wave 0's first
+// instruction) and end (every wave of it done, its stores landed), in ticks
+// of the device's constant-rate clock (s_memrealtime), stored by thread 0 as
+// two words at stamp[2 g], g the workgroup. Plain vector stores to a slot of
+// its own: no two workgroups touch one word, so stamping adds no contention.
+__device__ __forceinline__ void stamp_workgroup(unsigned long long *stamp, unsigned long long t0) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+        stamp[2 * blockIdx.x] = t0;
+        stamp[2 * blockIdx.x + 1] = t1;
+    }
+}
+
 }  // namespace
 }  // namespace w4a8
 
@@ -41,9 +56,18 @@ __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int 
 
 // One kernel per (step kind, activation format, coherence variant), named
 // w4a8_plan_<kind>_<format><variant>; chain_plan.hip builds the same names.
-#define W4A8_PLAN_KERNEL(NAME, XF, ARGMAX, PAIR, COH)                                          \
-    extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void NAME(W4A8_PLAN_ARGS) { \
-        w4a8::plan_step<XF, ARGMAX, PAIR, COH>(W4A8_PLAN_PASS);                                \
+// Each has a timed twin, <name>_t, for w4a8_chain_plan_launch_timed: the
+// same body, its workgroups' spans stamped through one more argument (the
+// plain kernels are untouched by it).
+#define W4A8_PLAN_KERNEL(NAME, XF, ARGMAX, PAIR, COH)                                                     \
+    extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void NAME(W4A8_PLAN_ARGS) {            \
+        w4a8::plan_step<XF, ARGMAX, PAIR, COH>(W4A8_PLAN_PASS);                                           \
+    }                                                                                                     \
+    extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void NAME##_t(W4A8_PLAN_ARGS,          \
+                                                                             unsigned long long *stamp) { \
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();                                   \
+        w4a8::plan_step<XF, ARGMAX, PAIR, COH>(W4A8_PLAN_PASS);                                           \
+        w4a8::stamp_workgroup(stamp, t0);                                                                 \
     }
 #define W4A8_PLAN_KIND(KIND, FMT, XF, ARGMAX, PAIR)                                            \
     W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT, XF, ARGMAX, PAIR, 0)                            \

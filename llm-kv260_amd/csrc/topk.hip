@@ -252,7 +252,11 @@ std::atomic<void *> g_scratch[SCRATCH_MAX_DEVICES];
 std::mutex g_scratch_mu;
 
 // The device address of `scratch` on the current device, looked up once per
-// device (the first call on it) and kept.
+// device (the first call on it) and kept. The lookup is no stream work, but
+// it may load the library's code object on that device; under a stream
+// capture in global mode such a call could invalidate the capture, so this
+// thread's capture mode is relaxed around it (and restored), which lets the
+// first call on a device itself be captured.
 hipError_t scratch_of_current_device(void **out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -263,7 +267,12 @@ hipError_t scratch_of_current_device(void **out) {
         std::lock_guard<std::mutex> lock(g_scratch_mu);
         p = g_scratch[dev].load(std::memory_order_relaxed);
         if (!p) {
+            hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+            e = hipThreadExchangeStreamCaptureMode(&mode);
+            if (e != hipSuccess) return e;
             e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            const hipError_t back = hipThreadExchangeStreamCaptureMode(&mode);
+            if (e == hipSuccess) e = back;
             if (e != hipSuccess) return e;
             if (!p) return hipErrorInvalidSymbol;
             g_scratch[dev].store(p, std::memory_order_release);

@@ -45,7 +45,8 @@ EXPORTS = (
     "w4a8_gemv_gate_up_silu_q8_0",
     "w4a8_chain_set_mode", "w4a8_chain_set_spin_limit", "w4a8_chain_timeouts",
     "w4a8_chain_plan_create", "w4a8_chain_plan_create_steps", "w4a8_chain_plan_launch", "w4a8_chain_plan_wait",
-    "w4a8_chain_plan_destroy",
+    "w4a8_chain_plan_destroy", "w4a8_chain_plan_launch_timed", "w4a8_chain_plan_workgroups",
+    "w4a8_wall_clock_hz",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
     "w4a8_gguf_data_offset", "w4a8_gguf_find_key", "w4a8_gguf_find_tensor", "w4a8_gguf_key",
@@ -146,6 +147,12 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).restype = i
     L.w4a8_chain_plan_destroy.argtypes = [p]
     L.w4a8_chain_plan_destroy.restype = i
+    L.w4a8_chain_plan_launch_timed.argtypes = [p, i, p]
+    L.w4a8_chain_plan_launch_timed.restype = i
+    L.w4a8_chain_plan_workgroups.argtypes = [p, i]
+    L.w4a8_chain_plan_workgroups.restype = ctypes.c_long
+    L.w4a8_wall_clock_hz.argtypes = [ctypes.POINTER(ctypes.c_int64)]
+    L.w4a8_wall_clock_hz.restype = i
     _lib = L
     return L
 

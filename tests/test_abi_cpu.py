@@ -116,6 +116,51 @@ def test_argument_checks_come_before_the_device():
     assert L.w4a8_chain_plan_create_steps(ctypes.cast(one, ctypes.c_void_p), 1, ctypes.byref(plan)) == -2
     one = (S * 1)(S(kv260gemv.PLAN_GATE_UP_SILU_Q8, fake, fake, fake, 64, 4096, None, 0.0))
     assert L.w4a8_chain_plan_create_steps(ctypes.cast(one, ctypes.c_void_p), 1, ctypes.byref(plan)) == -2
+    assert L.w4a8_chain_plan_launch_timed(None, 1, fake) == -1
+    assert L.w4a8_chain_plan_workgroups(None, 0) == -1
+    assert L.w4a8_wall_clock_hz(None) == -1
+
+
+def test_plan_and_chain_range_checks_come_before_the_device():
+    """What a plan step may not write over, refused (-2) before any HIP call:
+    its own x; any step's weights, norm_w, argmax row or workspace. The same
+    steps with the ranges apart pass the checks and only then fail for want
+    of a device (-5). The stream chain refuses a step in place, and the batch
+    any output over an input or another output."""
+    L = kv260gemv.lib()
+    S = kv260gemv.PlanStep
+    k, rows = 2048, 64
+    wb = rows * k // 32 * 18
+    W, X, Y, N, A, WS, Y2 = (0x100000 * (i + 1) for i in range(7))
+    plan = ctypes.c_void_p()
+
+    def create(*steps):
+        arr = (S * len(steps))(*steps)
+        return L.w4a8_chain_plan_create_steps(ctypes.cast(arr, ctypes.c_void_p), len(steps), ctypes.byref(plan))
+
+    gemv = lambda w, x, y, norm=None: S(kv260gemv.PLAN_GEMV, w, x, y, rows, k, norm, 1e-5)
+    lm = lambda y, a, ws: S(kv260gemv.PLAN_ARGMAX, W, X, y, rows, k, None, 0.0, a, ws)
+    assert create(gemv(W, X, Y), gemv(W, Y, Y2)) == -5            # y feeds x: allowed
+    assert create(gemv(W, X, Y), gemv(W, X, Y + 64)) == -5        # outputs sharing bytes: allowed
+    assert create(gemv(W, X, X + 16)) == -2                       # x over its own y
+    assert create(gemv(W, X, Y), gemv(Y - wb + 16, X, Y2)) == -2  # weights over another step's y
+    assert create(gemv(W, X, W + 64)) == -2                       # weights over its own y
+    assert create(gemv(W, X, Y), gemv(W, X, Y2, Y + 128)) == -2   # norm_w over a y
+    assert create(gemv(W, X, Y, N), gemv(W, X, Y2, N)) == -5
+    assert create(gemv(W, X, Y), lm(Y2, Y + 8, WS)) == -2         # argmax row in a y
+    assert create(gemv(W, X, Y), lm(Y2, A, Y + 16)) == -2         # workspace over a y
+    assert create(gemv(W, X, Y), lm(Y2, A, WS)) == -5
+
+    class Step(ctypes.Structure):   # include/w4a8.h's w4a8_chain_step
+        _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                    ("rows", ctypes.c_int), ("k", ctypes.c_int)]
+
+    in_place = (Step * 2)(Step(W, X, Y, rows, k), Step(W, Y, Y + 8, rows, k))
+    assert L.w4a8_chain_gemv(ctypes.cast(in_place, ctypes.c_void_p), 2, None) == -2
+    batch = (Step * 2)(Step(W, X, Y, rows, k), Step(W, Y2, Y + 128, rows, k))
+    assert L.w4a8_gemv_batch(ctypes.cast(batch, ctypes.c_void_p), 2, None) == -2       # outputs overlap
+    batch = (Step * 2)(Step(W, X, Y, rows, k), Step(W, Y, Y2, rows, k))
+    assert L.w4a8_gemv_batch(ctypes.cast(batch, ctypes.c_void_p), 2, None) == -2       # y is another's x
 
 
 class Udmabuf(ctypes.Structure):

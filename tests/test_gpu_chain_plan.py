@@ -189,6 +189,44 @@ def test_plan_reader_paths(gpu):
     plan.close()
 
 
+def test_plan_steps_sharing_one_output_buffer(gpu):
+    """Three steps of different shapes write one buffer, as the reference's
+    caller gives every engine call the same y (board/tp/tp_llama.cpp:301):
+    gate|up's 16384 rows, then q|k|v's 3072 and o's 2048 over its start; two
+    readers then take k = 2048 slices of it as x (rows 0..2047, o's; rows
+    2048..4095, q|k|v's and then gate|up's). Each step maps its rows to other
+    workgroups (and XCDs), so the later writer's bytes must win everywhere:
+    byte-exact against the C oracle over 1 and 3 passes."""
+    import torch
+    k = 2048
+    shapes = [(16384, k), (3072, k), (k, k)]
+    mats, xs, _, wants = _independent(shapes, 2100)
+    shared = poisoned_f32(16384)
+    rd_blocks = [C.quantize_q4_0(O.normal_f32((k, k), 2150 + i, 0.02)) for i in range(2)]
+    rd_mats = [dev(b) for b in rd_blocks]
+    rd_ys = [poisoned_f32(k) for _ in range(2)]
+    final = np.array(wants[0], copy=True)
+    final[:3072] = wants[1]
+    final[:k] = wants[2]
+    rd_want = [C.gemv_q4_0(rd_blocks[i], k, *C.quantize_q8_0(np.ascontiguousarray(final[i * k:(i + 1) * k])))
+               for i in range(2)]
+    steps = (Step * 5)(*[Step(mats[i].data_ptr(), xs[i].data_ptr(), shared.data_ptr(), r, kk)
+                         for i, (r, kk) in enumerate(shapes)],
+                       *[Step(rd_mats[i].data_ptr(), shared[i * k:].data_ptr(), rd_ys[i].data_ptr(), k, k)
+                         for i in range(2)])
+    plan = Plan(gpu, steps, 5)
+    for passes in (1, 3):
+        shared.fill_(float("nan"))
+        for y in rd_ys:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        plan.run(passes)
+        assert_bytes_equal(host(shared), final, f"{passes} passes: the shared buffer")
+        for i in range(2):
+            assert_bytes_equal(host(rd_ys[i]), rd_want[i], f"{passes} passes: reader {i}")
+    plan.close()
+
+
 def test_plan_several_launches_one_wait(gpu):
     """Launches queue up; one wait covers them all; two plans share the queue."""
     shapes_a = [(2048, 2048), (16384, 2048)]

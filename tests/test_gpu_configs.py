@@ -152,6 +152,57 @@ def test_config3_decode_chain_400_steps(gpu, chain_blocks):
     check("batch")
 
 
+def test_config3_chain_plan_400_passes(gpu, chain_blocks):
+    """The headline issuer at full size: config 3's 65 matrices as a chain plan,
+    one pass, then 400 passes in one launch (26,000 packets, past the queue's
+    16,384-slot ring, so the launch waits for room in it), then two passes of
+    the timed launch; all 65 digests after each. The timed launch's stamps:
+    every dispatch's span is positive, and each dispatch starts after the one
+    before it ended (the packets' barrier bits)."""
+    import torch
+    chain, recs = cf.decode_chain(), FIX["config3"]
+    xs = [dev(cf.activation(m)) for m in chain]
+    ys = [poisoned_f32(m.rows) for m in chain]
+    steps = step_array(chain_blocks, xs, ys, [(m.rows, m.k) for m in chain])
+    L = gpu.lib()
+    torch.cuda.synchronize()
+    plan = ctypes.c_void_p()
+    gpu.check("w4a8_chain_plan_create", L.w4a8_chain_plan_create(ctypes.cast(steps, ctypes.c_void_p), len(chain),
+                                                                 ctypes.byref(plan)))
+    try:
+        for passes in (1, 400):
+            for y in ys:
+                y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            gpu.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, passes))
+            gpu.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
+            for m, y, rec in zip(chain, ys, recs):
+                assert sha(host(y)) == rec["y"], f"plan, {passes} passes: {m.name}"
+        for y in ys:
+            y.fill_(float("nan"))
+        grid = [L.w4a8_chain_plan_workgroups(plan, j) for j in range(len(chain))]
+        assert L.w4a8_chain_plan_workgroups(plan, -1) == sum(grid) and min(grid) > 0
+        stamps = torch.zeros(2 * 2 * sum(grid), dtype=torch.int64, device="cuda")
+        torch.cuda.synchronize()
+        gpu.check("w4a8_chain_plan_launch_timed", L.w4a8_chain_plan_launch_timed(plan, 2, stamps.data_ptr()))
+        gpu.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
+        for m, y, rec in zip(chain, ys, recs):
+            assert sha(host(y)) == rec["y"], f"timed plan: {m.name}"
+        wg = host(stamps).view(np.uint64).reshape(-1, 2).astype(np.int64)
+        assert (wg > 0).all() and (wg[:, 1] >= wg[:, 0]).all(), "every workgroup stamps its slot"
+        first = np.concatenate(([0], np.cumsum(grid * 2)[:-1]))
+        st = np.stack([np.minimum.reduceat(wg[:, 0], first), np.maximum.reduceat(wg[:, 1], first)], axis=1)
+        span = st[:, 1] - st[:, 0]
+        assert (span > 0).all(), span
+        assert (st[1:, 0] >= st[:-1, 1]).all(), "a dispatch started before the previous one ended"
+        hz = ctypes.c_int64()
+        gpu.check("w4a8_wall_clock_hz", L.w4a8_wall_clock_hz(ctypes.byref(hz)))
+        us = span / hz.value * 1e6
+        assert us.max() < 1000.0, us.max()
+    finally:
+        gpu.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
+
+
 def test_config3_one_launch_chain(gpu, chain_blocks):
     """The 65-matrix chain as one cooperative launch (W4A8_CHAIN_ONE_LAUNCH):
     byte-exact after the first launch and after 50 more, no wait given up."""
