@@ -669,7 +669,7 @@ def cpu_baseline(chain, mats, xs, budget_s=30.0):
     }
 
 
-def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph):
+def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph, overlapped=None):
     """The fields every bench line carries: the metric, the chain and its roofline."""
     plan = not args.no_plan
     n = len(cf.decode_chain())
@@ -696,7 +696,7 @@ def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd
                    "matrices_per_step": n, "weight_bytes_per_step": cf.chain_weight_bytes(),
                    "algorithmic_bytes_per_step": chain_bytes},
         "verified": (chain_check["ok"] and chain_check["weights_ok"] and chain_check.get("timed_launch_ok", True) and
-                     graph["verified"] and
+                     graph["verified"] and (overlapped is None or overlapped["verified"]) and
                      (one_launch is None or one_launch["verified"])),
         "roofline": {"bound": "hbm", "achieved": round(chain_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(chain_gbs / HBM_PEAK_GBS, 4),
@@ -717,19 +717,21 @@ def headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd
                   "verified": chain_check["ok"], "verification": chain_check,
                   "dependency": "matrix j+1 starts after matrix j's output is complete"},
         "chain_graph": graph,
+        "chain_overlapped": overlapped,
         "chain_one_launch": one_launch,
         "wall_s_timed": round(wall, 3),
     }
 
 
-def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph):
-    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, pmc_traffic() or {}, graph)
+def chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph, overlapped):
+    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, pmc_traffic() or {}, graph,
+                   overlapped)
     out["mode"] = "chain only: " + ("HIP graph" if args.no_plan else "plan, HIP graph") + (
         "" if one_launch is None else ", one-launch chain")
     return out
 
 
-def time_plan(torch, kv, L, ptr, n, steps, warmup, ys, check, stamp_passes):
+def time_plan(torch, kv, L, ptr, n, steps, warmup, ys, check, stamp_passes, overlapped=False):
     """ms per step of the chain plan: `warmup` passes, then exactly `steps`
     passes in one launch, waited for; the device is idle (synchronized) on
     both sides of the timed region and the outputs are poisoned before it;
@@ -739,7 +741,8 @@ def time_plan(torch, kv, L, ptr, n, steps, warmup, ys, check, stamp_passes):
     time."""
     import numpy as np
     plan = ctypes.c_void_p()
-    kv.check("w4a8_chain_plan_create", L.w4a8_chain_plan_create(ptr, n, ctypes.byref(plan)))
+    create = L.w4a8_chain_plan_create_overlapped if overlapped else L.w4a8_chain_plan_create
+    kv.check("w4a8_chain_plan_create", create(ptr, n, ctypes.byref(plan)))
     stamps = None
     try:
         kv.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, max(warmup, 1)))
@@ -846,6 +849,19 @@ def main() -> int:
             if args.stamp_summary:
                 write_stamp_summary(args.stamp_summary, kd, sys.argv[1:])
 
+    overlapped = None
+    if not args.no_plan:
+        log(f"timing {args.steps} steps after {args.warmup} warm-up steps (overlapped chain plan)")
+        ms_ov, _, ov_check, _ = time_plan(torch, kv, L, ptr, n, args.steps, args.warmup, ys,
+                                          lambda: verify(chain_digests), 0, overlapped=True)
+        overlapped = {"us_per_step": round(ms_ov * 1e3, 2), "tokens_per_s": round(1e3 / ms_ov, 1),
+                      "gbps": round(chain_bytes / (ms_ov * 1e-3) / 1e9, 1),
+                      "hbm_frac": round(chain_bytes / (ms_ov * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                      "issued_by": "w4a8_chain_plan_create_overlapped: step j + 1 dispatched without the barrier bit, "
+                                   "its weight loads issued at once, x read after an in-kernel wait for step j",
+                      "verified": ov_check["ok"], "verification": ov_check}
+        log(f"chain (overlapped plan): {overlapped['us_per_step']} us/step, verified {overlapped['verified']}")
+
     log(f"timing {args.steps} steps after {args.warmup} warm-up steps (HIP graph replay of w4a8_chain_gemv)")
     g_chain = graph_of(torch, stream, [lambda s: kv.check("w4a8_chain_gemv", L.w4a8_chain_gemv(ptr, n, s))])
     ms_graph, wall_graph = time_replays(torch, stream, g_chain, args.steps, args.warmup, before=lambda: poison(ys))
@@ -896,7 +912,7 @@ def main() -> int:
             log(f"prefill {r['tokens']} tokens: {r['ms_per_prompt']} ms, {r['tokens_per_s']} tokens/s "
                 f"(vs {r['tokens'] * ms_per_step:.3f} ms as one decode step per token), verified {r['verified']}")
     if args.chain_only:
-        out = chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph)
+        out = chain_only_line(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, graph, overlapped)
         print(json.dumps(out), flush=True)
         return 0 if out["verified"] else 1
 
@@ -958,13 +974,13 @@ def main() -> int:
         log("CPU baseline (bounded sample)")
         cpu = cpu_baseline(chain, mats, xs)
     verified = (chain_check["ok"] and weights_ok and chain_check.get("timed_launch_ok", True) and
-                batch_check["ok"] and graph["verified"] and
+                batch_check["ok"] and graph["verified"] and (overlapped is None or overlapped["verified"]) and
                 fused_chain.get("plan", {}).get("verified", True) and
                 fused_chain["fp32_act"].get("plan", {}).get("verified", True) and
                 (one_launch is None or one_launch["verified"]) and
                 all(r["verified"] for r in gemm) and prefill[0]["verified"] is True)
 
-    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph)
+    out = headline(args, cf, ms_per_step, chain_gbs, chain_check, one_launch, wall, kd, traffic, graph, overlapped)
     out["verified"] = verified
     out["verification"] = {"chain": chain_check, "chain_graph": graph_check, "batch": batch_check,
                            "fused_chain_plan": fused_chain.get("plan", {}).get("verified"),

@@ -331,6 +331,23 @@ int w4a8_chain_plan_launch(w4a8_chain_plan *plan, int passes);
 int w4a8_chain_plan_wait(w4a8_chain_plan *plan, int timeout_ms);
 int w4a8_chain_plan_destroy(w4a8_chain_plan *plan);
 
+/* The same chain as a plan whose steps overlap: step j + 1's dispatch goes
+ * out without the barrier bit, so its workgroups start while step j still
+ * runs and issue their weight loads at once (weights never depend on the
+ * chain); each then waits, inside the kernel, until every workgroup of step
+ * j has stored its outputs and its flag (device-coherent flag bytes, one
+ * per workgroup), and only then reads x. The first step of each pass keeps
+ * the barrier bit, so passes never overlap. This is the GPU form of the
+ * reference engine fetching the next matrix during the current MAC
+ * (hls/gemv2/gemv2.h:1-3, board/tp/tp_llama.cpp:364-368). Every step is a
+ * plain GEMV (w4a8_chain_step; k in 2048..W4A8_MAX_K), outputs byte-identical
+ * to w4a8_chain_plan_create's; launch, wait and destroy as for any plan.
+ * Every in-kernel wait is bounded: one that gives up ends every other wait
+ * of the launch, the launch's outputs are then not valid, and
+ * w4a8_chain_plan_wait returns W4A8_ERR_TIMEOUT once for it. A timed launch
+ * of such a plan runs its steps with the barrier bit (no overlap). */
+int w4a8_chain_plan_create_overlapped(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan);
+
 /* A launch of the plan that also times each dispatch, from inside the
  * kernels (no tool intercepts the queue): the same kernels with the same
  * outputs, each workgroup reading the device's constant-rate clock when its

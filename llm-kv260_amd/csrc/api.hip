@@ -275,7 +275,24 @@ int w4a8_chain_plan_create_steps(const w4a8_plan_step *steps, int n, w4a8_chain_
     }
     if (int st = plan_check_ranges(steps, n)) return st;
     hipError_t he = hipSuccess;
-    const int st = chain_plan_create(steps, n, plan, he);
+    const int st = chain_plan_create(steps, n, false, plan, he);
+    return st == W4A8_ERR_HIP ? hip_status(he) : st;
+}
+
+int w4a8_chain_plan_create_overlapped(const w4a8_chain_step *steps, int n, w4a8_chain_plan **plan) {
+    if (!steps || !plan) return W4A8_ERR_NULL;
+    *plan = nullptr;
+    if (n < 1 || n > W4A8_CHAIN_MAX_STEPS) return W4A8_ERR_SHAPE;
+    w4a8_plan_step ps[W4A8_CHAIN_MAX_STEPS] = {};
+    for (int i = 0; i < n; ++i) {
+        if (int s = check_gemv(steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k, 16)) return s;
+        if (steps[i].k < 2048) return W4A8_ERR_SHAPE;
+        ps[i] = w4a8_plan_step{W4A8_PLAN_GEMV, steps[i].w, steps[i].x, steps[i].y, steps[i].rows, steps[i].k,
+                               nullptr, 0.0f, nullptr, nullptr};
+    }
+    if (int st = plan_check_ranges(ps, n)) return st;
+    hipError_t he = hipSuccess;
+    const int st = chain_plan_create(ps, n, true, plan, he);
     return st == W4A8_ERR_HIP ? hip_status(he) : st;
 }
 

@@ -47,6 +47,11 @@ struct w4a8_chain_plan {
     hsa_signal_t done{};                   // launches in flight
     char *timed_kargs = nullptr;           // the timed launch's, device memory: one block per dispatch
     size_t timed_bytes = 0;
+    // Overlapped plans: steps after the first of a pass go out without the
+    // barrier bit and wait in the kernel (gemv_m1_dev.h, StreamSync).
+    bool overlapped = false;
+    uint8_t *flags = nullptr;              // device memory: per-step flag bytes, then the abort word
+    uint32_t *abort_word = nullptr;
 };
 
 namespace w4a8 {
@@ -64,6 +69,11 @@ static_assert(sizeof(PlanArgs) == 176, "argument block of the plan's kernels");
 // The timed twins take one more argument after the block: the dispatch's
 // two stamp words.
 constexpr size_t TIMED_ARGS_BYTES = sizeof(PlanArgs) + sizeof(unsigned long long *);
+// The overlapped plan's kernels take the step-to-step wait's arguments after
+// the block.
+constexpr size_t STREAM_ARGS_BYTES = sizeof(PlanArgs) + sizeof(StreamSync);
+static_assert(STREAM_ARGS_BYTES <= 256, "argument slot");
+constexpr int STREAM_SPIN_LIMIT = 1 << 20;   // polls (each a device-coherent read) before a wait gives up
 constexpr size_t ARG_STRIDE = 256;
 constexpr uint32_t QUEUE_PACKETS = 16384;
 // Kernel variants: (kernel kind) x (x format) x (coherence), in
@@ -116,6 +126,9 @@ struct DeviceRuntime {
     // [0]: the kernels, [1]: their timed twins.
     uint64_t kobj[2][N_KERNELS]{};
     uint32_t group[2][N_KERNELS]{}, priv[2][N_KERNELS]{};
+    // The overlapped plan's GEMV kernels: [x format f32 / eng][coherence variant].
+    uint64_t kobj_s[2][4]{};
+    uint32_t group_s[2][4]{}, priv_s[2][4]{};
 };
 constexpr int MAX_DEVICES = 16;
 DeviceRuntime g_rt[MAX_DEVICES];
@@ -196,6 +209,24 @@ int runtime_of(int dev, DeviceRuntime *&out) {
             // implicit block) would find zeros there, so refuse the code object.
             if (kargs != (t ? TIMED_ARGS_BYTES : sizeof(PlanArgs))) return rt.status;
         }
+    for (int f = 0; f < 2; ++f)
+        for (int c = 0; c < 4; ++c) {
+            hsa_executable_symbol_t sym;
+            char name[64];
+            std::snprintf(name, sizeof name, "w4a8_plan_gemv_%s%s_s.kd", f ? "eng" : "f32", COH_NAMES[c]);
+            uint32_t kargs = 0;
+            if (hsa_executable_get_symbol_by_name(rt.exe, name, &rt.agent, &sym) != HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &rt.kobj_s[f][c]) !=
+                    HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE,
+                                               &rt.group_s[f][c]) != HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE,
+                                               &rt.priv_s[f][c]) != HSA_STATUS_SUCCESS ||
+                hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_KERNARG_SEGMENT_SIZE, &kargs) !=
+                    HSA_STATUS_SUCCESS ||
+                kargs != STREAM_ARGS_BYTES)
+                return rt.status;
+        }
     if (hsa_queue_create(rt.agent, QUEUE_PACKETS, HSA_QUEUE_TYPE_SINGLE, nullptr, nullptr, UINT32_MAX, UINT32_MAX,
                          &rt.queue) != HSA_STATUS_SUCCESS)
         return rt.status;
@@ -233,7 +264,11 @@ int plan_check_ranges(const w4a8_plan_step *steps, int n) {
     return W4A8_OK;
 }
 
-int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out, hipError_t &he) {
+int chain_plan_create(const w4a8_plan_step *steps, int n, bool overlapped, w4a8_chain_plan **out, hipError_t &he) {
+    if (overlapped)
+        for (int j = 0; j < n; ++j)
+            if ((steps[j].kind != W4A8_PLAN_GEMV && steps[j].kind != W4A8_PLAN_GEMV_ENGINE) || steps[j].norm_w)
+                return W4A8_ERR_SHAPE;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return W4A8_ERR_NODEV;
     DeviceRuntime *rt = nullptr;
@@ -241,6 +276,7 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
     auto *p = new w4a8_chain_plan();
     p->device = dev;
     p->n = n;
+    p->overlapped = overlapped;
     p->kind.assign(n, 0);
     // Which outputs another step reads, in this pass or the next: written
     // through, and read from the coherence point. Outputs that share bytes
@@ -313,16 +349,47 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out,
     }
     std::vector<char> host((size_t)n * ARG_STRIDE, 0);
     for (int j = 0; j < n; ++j) std::memcpy(host.data() + (size_t)j * ARG_STRIDE, &args[j], sizeof(PlanArgs));
+    if (overlapped) {
+        // Flag bytes: each step's run 256-byte aligned, then the abort word;
+        // all zero (no instance finished yet).
+        std::vector<size_t> off(n);
+        size_t total = 0;
+        for (int j = 0; j < n; ++j) {
+            off[j] = total;
+            total += ((size_t)p->grid[j] + 255) / 256 * 256;
+        }
+        hipError_t fe = hipMalloc(&p->flags, total + 256);
+        if (fe == hipSuccess) fe = hipMemset(p->flags, 0, total + 256);
+        if (fe == hipSuccess) fe = hipDeviceSynchronize();
+        if (fe != hipSuccess) {
+            if (p->flags) (void)hipFree(p->flags);
+            delete p;
+            he = fe;
+            return W4A8_ERR_HIP;
+        }
+        p->abort_word = reinterpret_cast<uint32_t *>(p->flags + total);
+        for (int j = 0; j < n; ++j) {
+            StreamSync S{};
+            S.prev = j > 0 ? p->flags + off[j - 1] : nullptr;
+            S.mine = p->flags + off[j];
+            S.abort = p->abort_word;
+            S.prev_groups = j > 0 ? (int)p->grid[j - 1] : 0;
+            S.spin_limit = STREAM_SPIN_LIMIT;
+            std::memcpy(host.data() + (size_t)j * ARG_STRIDE + sizeof(PlanArgs), &S, sizeof S);
+        }
+    }
     hipError_t e = hipHostMalloc(&p->kargs, host.size(), hipHostMallocCoherent);
     if (e == hipSuccess) std::memcpy(p->kargs, host.data(), host.size());
     if (e != hipSuccess) {
         if (p->kargs) (void)hipHostFree(p->kargs);
+        if (p->flags) (void)hipFree(p->flags);
         delete p;
         he = e;
         return W4A8_ERR_HIP;
     }
     if (hsa_signal_create(0, 0, nullptr, &p->done) != HSA_STATUS_SUCCESS) {
         (void)hipHostFree(p->kargs);
+        if (p->flags) (void)hipFree(p->flags);
         delete p;
         return W4A8_ERR_HSA;
     }
@@ -368,20 +435,26 @@ int issue(w4a8_chain_plan *p, int passes, KArgs kargs_of) {
         auto *pk = reinterpret_cast<hsa_kernel_dispatch_packet_t *>(q->base_address) + (idx & (q->size - 1));
         std::memset(reinterpret_cast<char *>(pk) + 4, 0, sizeof(*pk) - 4);
         const int v = p->kind[j];
+        // Overlapped plans (not the timed launch): every step but the first
+        // of a pass without the barrier bit; its kernel waits for the step
+        // before. The plain GEMV's variant index is (format) * 4 + coherence.
+        const bool stream = p->overlapped && !TIMED;
+        const int sf = (v / 4) % N_FORMATS == FMT_ENG ? 1 : 0, sc = v % 4;
         pk->workgroup_size_x = (uint16_t)p->threads[j];
         pk->workgroup_size_y = 1;
         pk->workgroup_size_z = 1;
         pk->grid_size_x = p->grid[j] * p->threads[j];
         pk->grid_size_y = 1;
         pk->grid_size_z = 1;
-        pk->private_segment_size = rt->priv[TIMED][v];
-        pk->group_segment_size = rt->group[TIMED][v] + p->group[j];
-        pk->kernel_object = rt->kobj[TIMED][v];
+        pk->private_segment_size = stream ? rt->priv_s[sf][sc] : rt->priv[TIMED][v];
+        pk->group_segment_size = (stream ? rt->group_s[sf][sc] : rt->group[TIMED][v]) + p->group[j];
+        pk->kernel_object = stream ? rt->kobj_s[sf][sc] : rt->kobj[TIMED][v];
         pk->kernarg_address = kargs_of(i);
         const bool first = i == 0, last = i == total - 1;
         if (last) pk->completion_signal = p->done;
+        const bool barrier = !stream || j == 0;
         const uint16_t header =
-            (uint16_t)((HSA_PACKET_TYPE_KERNEL_DISPATCH << HSA_PACKET_HEADER_TYPE) | (1 << HSA_PACKET_HEADER_BARRIER) |
+            (uint16_t)((HSA_PACKET_TYPE_KERNEL_DISPATCH << HSA_PACKET_HEADER_TYPE) | ((barrier ? 1 : 0) << HSA_PACKET_HEADER_BARRIER) |
                        ((first ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_NONE) << HSA_PACKET_HEADER_SCACQUIRE_FENCE_SCOPE) |
                        ((last ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_NONE) << HSA_PACKET_HEADER_SCRELEASE_FENCE_SCOPE));
         const uint32_t setup = 1u << HSA_KERNEL_DISPATCH_PACKET_SETUP_DIMENSIONS;
@@ -448,10 +521,23 @@ int chain_plan_wait(w4a8_chain_plan *p, int timeout_ms) {
     for (;;) {
         const hsa_signal_value_t v =
             hsa_signal_wait_scacquire(p->done, HSA_SIGNAL_CONDITION_LT, 1, 1000000, HSA_WAIT_STATE_ACTIVE);
-        if (v < 1) return W4A8_OK;
+        if (v < 1) break;
         if (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() > timeout_ms)
             return W4A8_ERR_TIMEOUT;
     }
+    if (p->overlapped) {
+        // A step-to-step wait that gave up: the launch's outputs are not
+        // valid. Reported once, the word cleared for the next launch.
+        uint32_t aborted = 0;
+        if (hipMemcpy(&aborted, p->abort_word, sizeof aborted, hipMemcpyDeviceToHost) != hipSuccess)
+            return W4A8_ERR_HIP;
+        if (aborted) {
+            const uint32_t zero = 0;
+            if (hipMemcpy(p->abort_word, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess) return W4A8_ERR_HIP;
+            return W4A8_ERR_TIMEOUT;
+        }
+    }
+    return W4A8_OK;
 }
 
 int chain_plan_destroy(w4a8_chain_plan *p) {
@@ -460,6 +546,7 @@ int chain_plan_destroy(w4a8_chain_plan *p) {
     hsa_signal_destroy(p->done);
     (void)hipHostFree(p->kargs);
     if (p->timed_kargs) (void)hipFree(p->timed_kargs);
+    if (p->flags) (void)hipFree(p->flags);
     delete p;
     return W4A8_OK;
 }

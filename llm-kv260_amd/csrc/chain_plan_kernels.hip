@@ -15,9 +15,9 @@
 namespace w4a8 {
 namespace {
 
-template <int XF, bool ARGMAX, int PAIR, int COH>
+template <int XF, bool ARGMAX, int PAIR, int COH, bool STREAM = false>
 __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int rows, int k, int C, int rpw, int tiles,
-                                          int nblocks, int nthreads, GemvParams &P) {
+                                          int nblocks, int nthreads, GemvParams &P, const StreamSync *S = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     P.seg[0] = w0;
     P.x = x;
@@ -26,7 +26,7 @@ __device__ __forceinline__ void plan_step(const uint8_t *w0, const void *x, int 
     P.C = C;
     P.rpw = rpw;
     P.tiles = tiles;
-    gemv_m1_body<XF, true, true, ARGMAX, PAIR, COH>(P, blockIdx.x, nblocks, nthreads, lds);
+    gemv_m1_body<XF, true, true, ARGMAX, PAIR, COH, STREAM>(P, blockIdx.x, nblocks, nthreads, lds, S);
 }
 
 // The timed twins' stamps: each workgroup's start (its wave 0's first
@@ -69,6 +69,19 @@ __device__ __forceinline__ void stamp_workgroup(unsigned long long *stamp, unsig
         w4a8::plan_step<XF, ARGMAX, PAIR, COH>(W4A8_PLAN_PASS);                                           \
         w4a8::stamp_workgroup(stamp, t0);                                                                 \
     }
+// The overlapped plan's kernels (the plain GEMV only): w4a8_plan_gemv_<format>
+// <variant>_s, the step-to-step wait through one more argument.
+#define W4A8_PLAN_STREAM_KERNEL(NAME, XF, COH)                                                       \
+    extern "C" __global__ __launch_bounds__(w4a8::MAX_THREADS) void NAME##_s(W4A8_PLAN_ARGS,      \
+                                                                             w4a8::StreamSync S) { \
+        w4a8::plan_step<XF, false, 0, COH, true>(W4A8_PLAN_PASS, &S);                                \
+    }
+#define W4A8_PLAN_STREAM_KIND(FMT, XF)                                                   \
+    W4A8_PLAN_STREAM_KERNEL(w4a8_plan_gemv_##FMT, XF, 0)                                 \
+    W4A8_PLAN_STREAM_KERNEL(w4a8_plan_gemv_##FMT##_xc, XF, w4a8::COH_X)                  \
+    W4A8_PLAN_STREAM_KERNEL(w4a8_plan_gemv_##FMT##_yc, XF, w4a8::COH_Y)                  \
+    W4A8_PLAN_STREAM_KERNEL(w4a8_plan_gemv_##FMT##_xyc, XF, w4a8::COH_X | w4a8::COH_Y)
+
 #define W4A8_PLAN_KIND(KIND, FMT, XF, ARGMAX, PAIR)                                            \
     W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT, XF, ARGMAX, PAIR, 0)                            \
     W4A8_PLAN_KERNEL(w4a8_plan_##KIND##_##FMT##_xc, XF, ARGMAX, PAIR, w4a8::COH_X)             \
@@ -89,3 +102,5 @@ W4A8_PLAN_KIND(pairq, f32, w4a8::X_F32, false, w4a8::PAIR_Q8)
 W4A8_PLAN_KIND(pairq, rms, w4a8::X_RMS, false, w4a8::PAIR_Q8)
 W4A8_PLAN_KIND(argmax, f32, w4a8::X_F32, true, 0)
 W4A8_PLAN_KIND(argmax, rms, w4a8::X_RMS, true, 0)
+W4A8_PLAN_STREAM_KIND(f32, w4a8::X_F32)
+W4A8_PLAN_STREAM_KIND(eng, w4a8::X_ENGINE)

@@ -263,8 +263,74 @@ __device__ __forceinline__ void argmax_finish(const GemvParams &P, unsigned long
 constexpr int COH_X = 1, COH_Y = 2;
 constexpr int PAIR_F32 = 1, PAIR_Q8 = 2;
 
-template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, int PAIR = 0, int COH = 0>
-__device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, int nthreads, uint8_t *lds) {
+// The overlapped chain plan's step-to-step wait (chain_plan.hip): a step's
+// dispatch goes out without the barrier bit, so its workgroups start while
+// the step before is still running. Each workgroup issues its weight loads
+// (weights never depend on the chain), then waits until every workgroup of
+// the step before has finished (a flag byte each), and only then loads and
+// stages x. Each workgroup of a step stores its own flag byte once its
+// outputs have landed: the instance number it finished, modulo 256, read
+// from that same byte when it starts (every instance of the step before has
+// the same workgroups, and passes do not overlap: the first step of each
+// pass keeps the barrier bit). Loads and stores of the flags are device-
+// coherent (sc1). Every wait is bounded: one that gives up sets the abort
+// word, which ends every other wait at once, and the plan reports it.
+struct StreamSync {
+    const uint8_t *prev;     // the previous step's flags (one byte per workgroup), or null
+    uint8_t *mine;           // this step's
+    uint32_t *abort;
+    int prev_groups;
+    int spin_limit;
+};
+
+// Wave 0 polls; every wave of the workgroup calls this once (it ends with a
+// workgroup barrier). Returns the flag value this workgroup stores at its end
+// (valid in wave 0).
+__device__ __forceinline__ uint32_t stream_wait(const StreamSync &S, int block, int wave, int lane) {
+    uint32_t target = 0;
+    if (wave == 0) {
+        const __amdgpu_buffer_rsrc_t mb = buffer_of(S.mine, (uint32_t)block + 1u);
+        const uint32_t e = __builtin_amdgcn_readfirstlane((uint32_t)__builtin_amdgcn_raw_buffer_load_b8(mb, block, 0, SC1));
+        target = (e + 1u) & 0xFFu;
+        if (S.prev) {
+            const uint32_t want = target * 0x01010101u;
+            const int words = (S.prev_groups + 3) >> 2;
+            const __amdgpu_buffer_rsrc_t pb = buffer_of(S.prev, 4u * (uint32_t)words);
+            const __amdgpu_buffer_rsrc_t ab = buffer_of(S.abort, 4u);
+            for (int spin = 0;; ++spin) {
+                bool done = true;
+                for (int w = lane; w < words; w += 64) {
+                    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(pb, 4 * w, 0, SC1);
+                    const int valid = S.prev_groups - 4 * w;
+                    const uint32_t mask = valid >= 4 ? ~0u : (1u << (8 * valid)) - 1u;
+                    if ((v & mask) != (want & mask)) done = false;
+                }
+                const uint32_t aborted = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_raw_buffer_load_b32(ab, 0, 0, SC1));
+                if (__builtin_amdgcn_ballot_w64(!done) == 0) break;
+                if (aborted != 0u) break;
+                if (spin >= S.spin_limit) {
+                    if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, ab, 0, 0, SC1);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    __syncthreads();
+    return target;
+}
+
+// After the workgroup's outputs have landed: its flag for the next step.
+__device__ __forceinline__ void stream_arrive(const StreamSync &S, int block, uint32_t target) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)target, buffer_of(S.mine, (uint32_t)block + 1u), block, 0, SC1);
+}
+
+template <int XF, bool PLAIN, bool ONE_PASS, bool ARGMAX = false, int PAIR = 0, int COH = 0, bool STREAM = false>
+__device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int nblocks, int nthreads, uint8_t *lds,
+                                             const StreamSync *S = nullptr) {
     const int nb = P.k >> 5;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -293,21 +359,32 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     const int n_my = tile >= P.tiles ? 0 : tile + tstride >= P.tiles ? 1 : (P.tiles - 1 - tile) / tstride + 1;
 
     // 1. The activation. Its loads go out before any weight tile's; the
-    // staging below waits for them only.
+    // staging below waits for them only. (STREAM: after the weight loads and
+    // the wait for the step before, since x may be that step's output.)
     XRaw<XF> xr;
     constexpr int XAUX = (COH & COH_X) ? SC1 : 0;
     // X_RMS with four threads per block (every launch shape at K = 2048):
     // each thread loads, squares and stages a quarter of a block.
     [[maybe_unused]] XQuarter xq;
     const bool quarter = XF == X_RMS && nthreads >= 4 * nb;
-    if constexpr (XF == X_RMS) {
-        if (quarter)
-            x_load_quarter<XAUX>(P.x, P.norm_w, P.k, tid >> 2, tid & 3, tid < 4 * nb, xq);
-        else
+    auto load_x = [&]() {
+        if constexpr (XF == X_RMS) {
+            if (quarter)
+                x_load_quarter<XAUX>(P.x, P.norm_w, P.k, tid >> 2, tid & 3, tid < 4 * nb, xq);
+            else
+                x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+        } else {
             x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
-    } else {
-        x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
-    }
+        }
+    };
+    if constexpr (!STREAM) load_x();
+    [[maybe_unused]] uint32_t flag = 0;
+    auto after_weights = [&]() {
+        if constexpr (STREAM) {
+            flag = stream_wait(*S, block, wave, lane);
+            load_x();
+        }
+    };
 
 
     uint32_t xv[8][8];
@@ -513,6 +590,7 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
         Tile buf[DEPTH];
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) load_tile<PLAIN>(P, tile + d * tstride, lane, buf[d]);
+        after_weights();
         stage_x();
         int done = 0;
         for (; done + DEPTH <= n_my; done += DEPTH) {
@@ -525,13 +603,18 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     } else if (n_my == 1) {
         Tile b;
         load_tile<PLAIN>(P, tile, lane, b);
+        after_weights();
         stage_x();
         step(b, last_t{});
     } else {
+        after_weights();
         stage_x();
     }
     if constexpr (ARGMAX) argmax_finish(P, best, nblocks, waves, lds);
-    if constexpr ((COH & COH_Y) != 0) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (STREAM)
+        stream_arrive(*S, block, flag);
+    else if constexpr ((COH & COH_Y) != 0)
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // The fields the first loads need (and the grid and workgroup sizes, which

@@ -114,7 +114,7 @@ hipError_t launch_chain_one(const w4a8_chain_step *steps, int n, hipStream_t str
 // The chain plan (chain_plan.hip): statuses as the C ABI's; a HIP error of
 // create comes back in `he` with W4A8_ERR_HIP.
 int plan_check_ranges(const w4a8_plan_step *steps, int n);   // before any device work
-int chain_plan_create(const w4a8_plan_step *steps, int n, w4a8_chain_plan **out, hipError_t &he);
+int chain_plan_create(const w4a8_plan_step *steps, int n, bool overlapped, w4a8_chain_plan **out, hipError_t &he);
 int chain_plan_launch(w4a8_chain_plan *p, int passes);
 int chain_plan_launch_timed(w4a8_chain_plan *p, int passes, unsigned long long *stamps, hipError_t &he);
 int chain_plan_steps(const w4a8_chain_plan *p);

@@ -45,7 +45,7 @@ EXPORTS = (
     "w4a8_gemv_gate_up_silu_q8_0",
     "w4a8_chain_set_mode", "w4a8_chain_set_spin_limit", "w4a8_chain_timeouts",
     "w4a8_chain_plan_create", "w4a8_chain_plan_create_steps", "w4a8_chain_plan_launch", "w4a8_chain_plan_wait",
-    "w4a8_chain_plan_destroy", "w4a8_chain_plan_launch_timed", "w4a8_chain_plan_workgroups",
+    "w4a8_chain_plan_destroy", "w4a8_chain_plan_create_overlapped", "w4a8_chain_plan_launch_timed", "w4a8_chain_plan_workgroups",
     "w4a8_wall_clock_hz",
     # w4a8_gguf.h
     "w4a8_gguf_open", "w4a8_gguf_close", "w4a8_gguf_version", "w4a8_gguf_n_tensors", "w4a8_gguf_n_kv",
@@ -139,7 +139,7 @@ def lib() -> ctypes.CDLL:
         getattr(L, f).restype = i
     L.w4a8_chain_timeouts.argtypes = []
     L.w4a8_chain_timeouts.restype = i
-    for f in ("w4a8_chain_plan_create", "w4a8_chain_plan_create_steps"):
+    for f in ("w4a8_chain_plan_create", "w4a8_chain_plan_create_steps", "w4a8_chain_plan_create_overlapped"):
         getattr(L, f).argtypes = [p, i, ctypes.POINTER(p)]
         getattr(L, f).restype = i
     for f in ("w4a8_chain_plan_launch", "w4a8_chain_plan_wait"):

@@ -34,13 +34,13 @@ def _steps(mats, xs, ys, shapes):
 
 
 class Plan:
-    def __init__(self, gpu, steps, n):
+    def __init__(self, gpu, steps, n, overlapped=False):
         import torch
         torch.cuda.synchronize()       # the plan's queue is not ordered with HIP streams
         self.L, self.gpu = gpu.lib(), gpu
         self.p = ctypes.c_void_p()
-        gpu.check("w4a8_chain_plan_create", self.L.w4a8_chain_plan_create(ctypes.cast(steps, ctypes.c_void_p), n,
-                                                                          ctypes.byref(self.p)))
+        create = self.L.w4a8_chain_plan_create_overlapped if overlapped else self.L.w4a8_chain_plan_create
+        gpu.check("w4a8_chain_plan_create", create(ctypes.cast(steps, ctypes.c_void_p), n, ctypes.byref(self.p)))
 
     def run(self, passes=1):
         self.gpu.check("w4a8_chain_plan_launch", self.L.w4a8_chain_plan_launch(self.p, passes))
@@ -72,13 +72,14 @@ SHAPES = {
 }
 
 
+@pytest.mark.parametrize("overlapped", [False, True], ids=["barrier", "overlapped"])
 @pytest.mark.parametrize("name", sorted(SHAPES))
-def test_plan_matches_oracle_and_chain(gpu, name):
+def test_plan_matches_oracle_and_chain(gpu, name, overlapped):
     import torch
     shapes = SHAPES[name]
     mats, xs, ys, wants = _independent(shapes, 1500)
     steps = _steps(mats, xs, ys, shapes)
-    plan = Plan(gpu, steps, len(shapes))
+    plan = Plan(gpu, steps, len(shapes), overlapped)
     plan.run(1)
     for i, (y, want) in enumerate(zip(ys, wants)):
         assert_bytes_equal(host(y), want, f"{name} step {i} {shapes[i]}")
@@ -111,8 +112,10 @@ def _dependent_oracle(blocks, shapes, x0, passes):
     return outs
 
 
-def test_plan_dependency_inside_a_pass(gpu):
-    """x of every step after the first IS the previous step's y."""
+@pytest.mark.parametrize("overlapped", [False, True], ids=["barrier", "overlapped"])
+def test_plan_dependency_inside_a_pass(gpu, overlapped):
+    """x of every step after the first IS the previous step's y (overlapped:
+    each step's workgroups start early and must wait for that y)."""
     shapes = [(2048, 2048), (8192, 2048), (2048, 8192), (2048, 2048), (3072, 2048), (2048, 3072), (2048, 2048)]
     blocks = [C.quantize_q4_0(O.normal_f32((r, k), 60 + i, 0.02)) for i, (r, k) in enumerate(shapes)]
     x0 = O.normal_f32((1, shapes[0][1]), 59)[0]
@@ -120,7 +123,7 @@ def test_plan_dependency_inside_a_pass(gpu):
     mats = [dev(b) for b in blocks]
     xin = dev(x0)
     ys = [poisoned_f32(r) for r, _ in shapes]
-    plan = Plan(gpu, _steps(mats, [xin] + ys[:-1], ys, shapes), len(shapes))
+    plan = Plan(gpu, _steps(mats, [xin] + ys[:-1], ys, shapes), len(shapes), overlapped)
     for passes in (1, 4, 2):
         for y in ys:
             y.fill_(float("nan"))
@@ -130,7 +133,8 @@ def test_plan_dependency_inside_a_pass(gpu):
     plan.close()
 
 
-def test_plan_dependency_across_passes(gpu):
+@pytest.mark.parametrize("overlapped", [False, True], ids=["barrier", "overlapped"])
+def test_plan_dependency_across_passes(gpu, overlapped):
     """The first step reads the last step's output: each pass continues from
     the previous one, within a launch and across launches."""
     shapes = [(8192, 2048), (2048, 8192), (3072, 2048), (2048, 3072)]
@@ -139,7 +143,7 @@ def test_plan_dependency_across_passes(gpu):
     mats = [dev(b) for b in blocks]
     ys = [poisoned_f32(r) for r, _ in shapes]
     ys[-1].copy_(dev(x0))                  # the first pass starts from x0
-    plan = Plan(gpu, _steps(mats, [ys[-1]] + ys[:-1], ys, shapes), len(shapes))
+    plan = Plan(gpu, _steps(mats, [ys[-1]] + ys[:-1], ys, shapes), len(shapes), overlapped)
     plan.run(3)
     wants = _dependent_oracle(blocks, shapes, x0, 3)
     for i, (y, want) in enumerate(zip(ys, wants)):
@@ -245,6 +249,35 @@ def test_plan_several_launches_one_wait(gpu):
         assert_bytes_equal(host(y), want, "queued launches")
     pa.close()
     pb.close()
+
+
+def test_overlapped_plan_timed_launch_and_checks(gpu):
+    """An overlapped plan's timed launch (barrier bits, no overlap) gives the
+    same outputs and leaves the flags consistent: a plain launch after it is
+    still byte-exact. Only plain GEMV steps are accepted."""
+    import torch
+    shapes = SHAPES["llama_layer"]
+    mats, xs, ys, wants = _independent(shapes, 1550)
+    plan = Plan(gpu, _steps(mats, xs, ys, shapes), len(shapes), overlapped=True)
+    L = gpu.lib()
+    stamps = torch.zeros(2 * 2 * L.w4a8_chain_plan_workgroups(plan.p, -1), dtype=torch.int64, device="cuda")
+    for y in ys:
+        y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    gpu.check("launch_timed", L.w4a8_chain_plan_launch_timed(plan.p, 2, stamps.data_ptr()))
+    gpu.check("wait", L.w4a8_chain_plan_wait(plan.p, 30000))
+    for i, (y, want) in enumerate(zip(ys, wants)):
+        assert_bytes_equal(host(y), want, f"timed, step {i}")
+    for y in ys:
+        y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    plan.run(3)
+    for i, (y, want) in enumerate(zip(ys, wants)):
+        assert_bytes_equal(host(y), want, f"after the timed launch, step {i}")
+    plan.close()
+    p = ctypes.c_void_p()
+    bad = _steps(mats, xs, ys, [(64, 1024)])
+    assert L.w4a8_chain_plan_create_overlapped(ctypes.cast(bad, ctypes.c_void_p), 1, ctypes.byref(p)) == -2
 
 
 def test_plan_argument_checks(gpu):

@@ -203,6 +203,33 @@ def test_config3_chain_plan_400_passes(gpu, chain_blocks):
         gpu.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
 
 
+def test_config3_overlapped_plan_400_passes(gpu, chain_blocks):
+    """Config 3's 65 matrices as an overlapped plan (each step's workgroups
+    start during the step before and wait for it in the kernel): all 65
+    digests after one pass and after 400 passes in one launch."""
+    import torch
+    chain, recs = cf.decode_chain(), FIX["config3"]
+    xs = [dev(cf.activation(m)) for m in chain]
+    ys = [poisoned_f32(m.rows) for m in chain]
+    steps = step_array(chain_blocks, xs, ys, [(m.rows, m.k) for m in chain])
+    L = gpu.lib()
+    torch.cuda.synchronize()
+    plan = ctypes.c_void_p()
+    gpu.check("w4a8_chain_plan_create_overlapped",
+              L.w4a8_chain_plan_create_overlapped(ctypes.cast(steps, ctypes.c_void_p), len(chain), ctypes.byref(plan)))
+    try:
+        for passes in (1, 400):
+            for y in ys:
+                y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            gpu.check("w4a8_chain_plan_launch", L.w4a8_chain_plan_launch(plan, passes))
+            gpu.check("w4a8_chain_plan_wait", L.w4a8_chain_plan_wait(plan, 60000))
+            for m, y, rec in zip(chain, ys, recs):
+                assert sha(host(y)) == rec["y"], f"overlapped plan, {passes} passes: {m.name}"
+    finally:
+        gpu.check("w4a8_chain_plan_destroy", L.w4a8_chain_plan_destroy(plan))
+
+
 def test_config3_one_launch_chain(gpu, chain_blocks):
     """The 65-matrix chain as one cooperative launch (W4A8_CHAIN_ONE_LAUNCH):
     byte-exact after the first launch and after 50 more, no wait given up."""
