@@ -795,6 +795,9 @@ def main() -> int:
     ap.add_argument("--no-plan", action="store_true",
                     help="time the chain through w4a8_chain_gemv only (the headline then comes from the HIP "
                          "graph)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time the M > 1 sweep (configuration 4) and stop: the run the GEMM's counter summaries "
+                         "are taken from")
     ap.add_argument("--stamp-passes", type=int, default=100,
                     help="passes of the plan's timed launch (in-kernel dispatch spans; 0 = none)")
     ap.add_argument("--stamp-summary", default=None, metavar="PATH",
@@ -824,6 +827,19 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"calibration copy: {args.copy_calibration} MB")
         del src, dst
+    if args.gemm_only:
+        g4 = {(r["name"], r["m"]): r for r in fixtures()["config4"]}
+        gemm = []
+        for m, base in zip(cf.GEMM_SHAPES, seeded_blocks(torch, kv, cf, cf.GEMM_SHAPES)):
+            for mrows in cf.GEMM_M:
+                r = time_gemm(torch, kv, cf, m, mrows, stream, base, g4[(m.name, mrows)])
+                gemm.append(dict(name=m.name, **r))
+                log(f"gemm {m.name} M={mrows}: {r['us']} us, verified {r['verified']}")
+            del base
+            torch.cuda.empty_cache()
+        ok = all(r["verified"] for r in gemm)
+        print(json.dumps({"mode": "gemm only", "gemm": gemm, "verified": ok}), flush=True)
+        return 0 if ok else 1
     log("building the 65-matrix decode chain (config 3's seeded weights) on the device")
     chain, mats, xs, ys, steps, recs, weights_ok = build_chain(torch, kv, cf)
     n = len(chain)
