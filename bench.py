@@ -620,7 +620,7 @@ def write_stamp_summary(path, kd, argv):
     lines += ["",
               f"sum of the 65 spans per step: {kd['sum_us_per_step']} us (median {kd['median_sum_us_per_step']}), "
               f"{kd['achieved']} GB/s, frac {kd['frac']}",
-              f"boundary (last wave end -> next first wave start): mean {kd['gap_us_mean']} us, "
+              f"boundary (last workgroup end -> next dispatch's first workgroup start): mean {kd['gap_us_mean']} us, "
               f"median {kd['gap_us_median']} us",
               f"first start -> last end per step: {kd['first_start_to_last_end_us_per_step']} us; "
               f"timed launch {kd['timed_launch_us_per_step']} us/step (host clock); "
