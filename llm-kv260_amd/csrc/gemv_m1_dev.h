@@ -367,12 +367,24 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
     // each thread loads, squares and stages a quarter of a block.
     [[maybe_unused]] XQuarter xq;
     const bool quarter = XF == X_RMS && nthreads >= 4 * nb;
+    // X_F32 with a thread per block: by whole lines, in the waves that hold
+    // blocks only (a wave-uniform branch: the others issue no activation
+    // load at all).
+    [[maybe_unused]] XLines xl;
+    const bool lines = XF == X_F32 && nthreads >= nb;
+    const bool x_wave = __builtin_amdgcn_readfirstlane(wave) * 64 < nb;
     auto load_x = [&]() {
         if constexpr (XF == X_RMS) {
             if (quarter)
                 x_load_quarter<XAUX>(P.x, P.norm_w, P.k, tid >> 2, tid & 3, tid < 4 * nb, xq);
             else
                 x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+        } else if constexpr (XF == X_F32) {
+            if (lines) {
+                if (x_wave) x_load_lines<XAUX>(P.x, P.k, wave, lane, xl);
+            } else {
+                x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
+            }
         } else {
             x_load<XF, XAUX>(P.x, P.k, tid, tid < nb, xr, P.norm_w);
         }
@@ -446,6 +458,9 @@ __device__ __forceinline__ void gemv_m1_body(const GemvParams &P, int block, int
                 if (tid < 4 * nb) x_stage_quarter(xq, tid >> 2, tid & 3, s_x, rms);
             }
         } else {
+            if constexpr (XF == X_F32) {
+                if (lines && x_wave) x_lines_to_block(xl, lane, slab, xr);
+            }
             if (tid < nb) x_stage<XF>(xr, tid, s_x, rms);
             for (int b = tid + nthreads; b < nb; b += nthreads) {   // only if a launch has fewer threads than blocks
                 XRaw<XF> xb;

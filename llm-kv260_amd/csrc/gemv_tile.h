@@ -71,6 +71,43 @@ __device__ __forceinline__ void load_f32_block(__amdgpu_buffer_rsrc_t rb, int of
     }
 }
 
+// An fp32 x read by whole lines: wave w takes blocks 64 w .. 64 w + 63, and
+// its instruction m gives lane l the 16 bytes at 8192 w + 1024 m + 16 l
+// (block 64 w + 8 m + l / 8, piece l % 8), so that every instruction reads 1
+// KB of consecutive bytes. Loaded one block per lane (128 bytes apart), each
+// instruction touched 64 lines and the memory pipeline took about 64 clocks
+// for it, so that a wave's weight loads queued behind its activation's.
+// Bytes past x read zeros.
+struct XLines {
+    u32x4 v[8];
+};
+
+template <int AUX = 0>
+__device__ __forceinline__ void x_load_lines(const void *x, int k, int wave, int lane, XLines &r) {
+    const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)(4 * k));
+    const int base = 8192 * wave + 16 * lane;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) r.v[m] = __builtin_amdgcn_raw_buffer_load_b128(xb, base + 1024 * m, 0, AUX);
+}
+
+// The lines regrouped one block per lane through `tmp`, 9,216 bytes of LDS
+// that only this wave uses (144 bytes per block: both the writes and the
+// reads spread over the banks): lane l then holds block 64 w + l as x_load
+// delivers it.
+__device__ __forceinline__ void x_lines_to_block(const XLines &r, int lane, uint8_t *tmp, XRaw<X_F32> &out) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+        *reinterpret_cast<u32x4 *>(tmp + 144 * (8 * m + (lane >> 3)) + 16 * (lane & 7)) = r.v[m];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const u32x4 t = *reinterpret_cast<const u32x4 *>(tmp + 144 * lane + 16 * j);
+        out.v[j] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
+    }
+}
+
 // Block b of the activation; a lane with live == false reads nothing. AUX:
 // the cache policy of the fp32 x's loads (SC1: from the device's coherence
 // point, for an x that an earlier dispatch with no fence after it wrote).
