@@ -4,14 +4,26 @@
  * Drop-in for board/kv260gemv/udmabuf.h:15-36. On the board a pool is CMA
  * memory the CPU and the fabric share, and clean/invalidate are cache
  * maintenance. On the GPU a pool is two allocations of the same size: device
- * memory in HBM (what the engine reads and writes; `phys` is its device
- * address) and a pinned host mirror (`base`, what the CPU code touches).
- *   - udmabuf_clean(p, len)      copies [p, p+len) host -> device
- *   - udmabuf_invalidate(p, len) copies [p, p+len) device -> host
- * both synchronously, so the reference's discipline ("clean before the engine
- * reads what the CPU wrote, invalidate before the CPU reads what the engine
- * wrote") carries the data exactly where it did on the board. Pointers outside
- * every open pool are ignored, as cache maintenance on them would be.
+ * memory in HBM (what the engine reads; `phys` is its device address) and a
+ * pinned host copy (`base`, what the CPU code touches), mapped for the GPU and
+ * coherent. The library tracks which copy of each range is current:
+ *   - udmabuf_clean(p, len): the CPU wrote [p, p+len). Under 1 MiB nothing is
+ *     copied yet: the range is marked host-current, and the next engine call
+ *     that reads it (as x or as weights) copies it to the device first, on
+ *     the engine's stream, ahead of the GEMV. From 1 MiB on (weights after
+ *     loading) it is copied host -> device at once, synchronously.
+ *   - an engine call writes its y straight into the host copy (the GPU's
+ *     stores cross PCIe as the GEMV makes them), so y's range is
+ *     host-current once the call's wait returns.
+ *   - udmabuf_invalidate(p, len): the CPU will read [p, p+len). The parts
+ *     not host-current are copied device -> host, synchronously (the device
+ *     copy may hold writes made outside the engine calls); host-current parts
+ *     need nothing.
+ * So the reference's discipline ("clean before the engine reads what the CPU
+ * wrote, invalidate before the CPU reads what the engine wrote") still carries
+ * the data exactly where it did on the board, and its per-call clean of x and
+ * invalidates of y cost no copy of their own. Pointers outside every open pool
+ * are ignored, as cache maintenance on them would be.
  *
  * Pool sizes: KV260GEMV_UDMABUF_SIZES, e.g. "udmabuf0=1G,udmabuf1=256M"
  * (K/M/G suffixes); default udmabuf0 = 1 GiB and no other pool, so

@@ -14,6 +14,8 @@
 #include "../../include/gemv_dev.h"
 #include "../../include/udmabuf.h"
 #include "kernels.h"
+#include "pool_ranges.h"
+#include "q4_0_device.h"
 
 using namespace w4a8;
 
@@ -119,22 +121,107 @@ void check_w(const uint64_t *w, int n, const char *who) {
         if (!w[i] || (w[i] & 15)) die(who, "weight address NULL or not 16-byte aligned");
 }
 
-void start(EngineCtx *c, const MatrixRef &m, uint64_t x, uint64_t y, const char *who) {
-    check_hip(hipSetDevice(c->device), who);
-    check_hip(launch_gemv_m1(m, (const void *)(uintptr_t)x, X_ENGINE, (float *)(uintptr_t)y, c->stream), who);
-}
-
 // ------------------------------------------------------------------ pools
+//
+// A pool is device memory (what the engine reads; its addresses are the
+// "physical" ones handed to the engine) and pinned host memory of the same
+// size (what the CPU touches), mapped for the GPU and coherent. Which copy of
+// a range is current:
+//  * udmabuf_clean of a range under EAGER_CLEAN bytes copies nothing: the
+//    range joins the pool's host-current set (a larger clean, such as the
+//    weights once after loading, is copied at once);
+//  * an engine call first copies the host-current parts of what it reads
+//    (its weights and x) to the device, on its own stream, ahead of the
+//    GEMV, and writes its y straight into the host copy, so that y's range
+//    is host-current afterwards;
+//  * udmabuf_invalidate copies to the host only the parts that are not
+//    host-current (the device copy of those may hold writes made outside
+//    the engine calls).
+// The reference caller's per-call clean of x and its invalidates of y before
+// and after the call then cost no copy of their own; x's copy rides on the
+// engine's stream ahead of the GEMV, and y's bytes go to the host as the
+// GEMV writes them.
+
+constexpr size_t EAGER_CLEAN = (size_t)1 << 20;
 
 struct Pool {
     uint8_t *host;
     uint8_t *dev;
     size_t size;
     int device;
+    uint8_t *host_dev;                          // the host memory's address on the GPU
+    pool_ranges::Set *host_cur;                 // the host-current ranges (offsets)
 };
 constexpr int MAX_POOLS = 16;
 Pool g_pools[MAX_POOLS];
 std::mutex g_pool_mu;
+
+// Bytes [a, b) of src to dst (the same offsets in both): 16-byte pieces, the
+// unaligned head and tail byte by byte.
+__global__ void copy_range_kernel(uint8_t *dst, const uint8_t *src, size_t a, size_t b) {
+    const size_t a16 = (a + 15) & ~(size_t)15, b16 = b & ~(size_t)15;
+    const size_t i = a16 + 16 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (a16 < b16 && i < b16) *reinterpret_cast<uint4 *>(dst + i) = *reinterpret_cast<const uint4 *>(src + i);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const size_t head = a16 < b ? a16 : b;
+        for (size_t j = a; j < head; ++j) dst[j] = src[j];
+        for (size_t j = (b16 > head ? b16 : head); j < b; ++j) dst[j] = src[j];
+    }
+}
+
+// The pool whose device memory holds [phys, phys + len), or null.
+Pool *pool_of_dev(uint64_t phys, size_t len, size_t *off) {
+    const uint8_t *a = (const uint8_t *)(uintptr_t)phys;
+    for (auto &pl : g_pools) {
+        if (!pl.host || a < pl.dev || a >= pl.dev + pl.size) continue;
+        *off = (size_t)(a - pl.dev);
+        if (len > pl.size - *off) return nullptr;
+        return &pl;
+    }
+    return nullptr;
+}
+
+// Before an engine call on `stream`: the host-current parts of a range it reads go to the device.
+void flush_reads(uint64_t phys, size_t len, hipStream_t stream, const char *who) {
+    std::lock_guard<std::mutex> g(g_pool_mu);
+    size_t off;
+    Pool *pl = pool_of_dev(phys, len, &off);
+    if (!pl || pl->host_cur->empty()) return;
+    for (const auto &r : pool_ranges::parts(*pl->host_cur, off, off + len, true)) {
+        const size_t n = r.second - r.first;
+        if (n >= EAGER_CLEAN) {
+            check_hip(hipMemcpyAsync(pl->dev + r.first, pl->host + r.first, n, hipMemcpyHostToDevice, stream), who);
+        } else {
+            const size_t units = (n + 15) / 16 + 1;
+            const unsigned grid = (unsigned)((units + 255) / 256);
+            hipLaunchKernelGGL(copy_range_kernel, dim3(grid), dim3(256), 0, stream, pl->dev, pl->host_dev, r.first,
+                               r.second);
+            check_hip(hipGetLastError(), who);
+        }
+    }
+    pool_ranges::remove(*pl->host_cur, off, off + len);
+}
+
+// y of an engine call: its address in the host copy when it lies in a pool
+// (the range is host-current from then on), else y itself.
+float *route_y(uint64_t y, int rows) {
+    std::lock_guard<std::mutex> g(g_pool_mu);
+    size_t off;
+    const size_t len = (size_t)rows * 4;
+    Pool *pl = pool_of_dev(y, len, &off);
+    if (!pl) return (float *)(uintptr_t)y;
+    pool_ranges::add(*pl->host_cur, off, off + len);
+    return reinterpret_cast<float *>(pl->host_dev + off);
+}
+
+void start(EngineCtx *c, const MatrixRef &m, uint64_t x, uint64_t y, const char *who) {
+    check_hip(hipSetDevice(c->device), who);
+    const size_t seg_bytes = (size_t)m.seg_rows * (size_t)(m.k / QK) * Q4_0_BYTES;
+    for (int q = 0; q < m.nseg; ++q) flush_reads((uint64_t)(uintptr_t)m.seg[q], seg_bytes, c->stream, who);
+    flush_reads(x, (size_t)m.k + (size_t)m.k / 8, c->stream, who);
+    float *yp = route_y(y, m.rows);
+    check_hip(launch_gemv_m1(m, (const void *)(uintptr_t)x, X_ENGINE, yp, c->stream), who);
+}
 
 size_t parse_size(const char *s, const char *end) {
     char *e = nullptr;
@@ -164,18 +251,17 @@ size_t pool_size(const char *name) {
     return 0;
 }
 
-// The pool holding host address p, clamped range [off, off + len).
-bool find_pool(const void *p, size_t len, Pool *out, size_t *off, size_t *n) {
+// The pool holding host address p, clamped range [off, off + len); called
+// with g_pool_mu held.
+Pool *find_pool(const void *p, size_t len, size_t *off, size_t *n) {
     const uint8_t *a = (const uint8_t *)p;
-    std::lock_guard<std::mutex> g(g_pool_mu);
     for (auto &pl : g_pools) {
         if (!pl.host || a < pl.host || a >= pl.host + pl.size) continue;
-        *out = pl;
         *off = (size_t)(a - pl.host);
         *n = len < pl.size - *off ? len : pl.size - *off;
-        return true;
+        return &pl;
     }
-    return false;
+    return nullptr;
 }
 
 }  // namespace
@@ -324,9 +410,18 @@ int udmabuf_open(udmabuf_t *b, const char *name) {
         fprintf(stderr, "udmabuf: cannot allocate %zu MB of device memory for %s\n", size >> 20, name);
         return -1;
     }
-    if (hipHostMalloc(&host, size, hipHostMallocDefault) != hipSuccess) {
+    if (hipHostMalloc(&host, size, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
         (void)hipFree(devp);
         fprintf(stderr, "udmabuf: cannot allocate %zu MB of pinned host memory for %s\n", size >> 20, name);
+        return -1;
+    }
+    void *host_dev = nullptr;
+    auto *cur = new (std::nothrow) pool_ranges::Set();
+    if (!cur || hipHostGetDevicePointer(&host_dev, host, 0) != hipSuccess) {
+        delete cur;
+        (void)hipHostFree(host);
+        (void)hipFree(devp);
+        fprintf(stderr, "udmabuf: cannot map the host memory of %s for the device\n", name);
         return -1;
     }
     {
@@ -335,12 +430,13 @@ int udmabuf_open(udmabuf_t *b, const char *name) {
         for (int i = 0; i < MAX_POOLS; ++i)
             if (!g_pools[i].host) { slot = i; break; }
         if (slot < 0) {
+            delete cur;
             (void)hipHostFree(host);
             (void)hipFree(devp);
             fprintf(stderr, "udmabuf: more than %d pools open\n", MAX_POOLS);
             return -1;
         }
-        g_pools[slot] = Pool{(uint8_t *)host, (uint8_t *)devp, size, dev};
+        g_pools[slot] = Pool{(uint8_t *)host, (uint8_t *)devp, size, dev, (uint8_t *)host_dev, cur};
     }
     b->fd = dev;
     b->base = (uint8_t *)host;
@@ -364,6 +460,7 @@ void udmabuf_close(udmabuf_t *b) {
             (void)hipDeviceSynchronize();
             (void)hipHostFree(found.host);
             (void)hipFree(found.dev);
+            delete found.host_cur;
         }
     }
     memset(b, 0, sizeof *b);
@@ -379,19 +476,30 @@ void *udmabuf_alloc(udmabuf_t *b, size_t size, size_t align) {
 }
 
 void udmabuf_clean(const void *p, size_t len) {
-    Pool pl;
+    std::lock_guard<std::mutex> g(g_pool_mu);
     size_t off, n;
-    if (!len || !find_pool(p, len, &pl, &off, &n)) return;
-    check_hip(hipSetDevice(pl.device), "udmabuf_clean");
-    check_hip(hipMemcpy(pl.dev + off, pl.host + off, n, hipMemcpyHostToDevice), "udmabuf_clean");
+    Pool *pl = len ? find_pool(p, len, &off, &n) : nullptr;
+    if (!pl) return;
+    if (n < EAGER_CLEAN) {
+        pool_ranges::add(*pl->host_cur, off, off + n);
+        return;
+    }
+    check_hip(hipSetDevice(pl->device), "udmabuf_clean");
+    check_hip(hipMemcpy(pl->dev + off, pl->host + off, n, hipMemcpyHostToDevice), "udmabuf_clean");
+    pool_ranges::remove(*pl->host_cur, off, off + n);
 }
 
 void udmabuf_invalidate(const void *p, size_t len) {
-    Pool pl;
+    std::lock_guard<std::mutex> g(g_pool_mu);
     size_t off, n;
-    if (!len || !find_pool(p, len, &pl, &off, &n)) return;
-    check_hip(hipSetDevice(pl.device), "udmabuf_invalidate");
-    check_hip(hipMemcpy(pl.host + off, pl.dev + off, n, hipMemcpyDeviceToHost), "udmabuf_invalidate");
+    Pool *pl = len ? find_pool(p, len, &off, &n) : nullptr;
+    if (!pl) return;
+    const auto parts = pool_ranges::parts(*pl->host_cur, off, off + n, false);
+    if (parts.empty()) return;
+    check_hip(hipSetDevice(pl->device), "udmabuf_invalidate");
+    for (const auto &r : parts)
+        check_hip(hipMemcpy(pl->host + r.first, pl->dev + r.first, r.second - r.first, hipMemcpyDeviceToHost),
+                  "udmabuf_invalidate");
 }
 
 }  // extern "C"
