@@ -186,10 +186,12 @@ def test_gemv_random_bytes(gpu):
 
 
 def test_gemv_nonfinite_scales(gpu):
-    """Infinite and NaN fp16 scales: every output the contract leaves finite or infinite is
-    byte-identical; where the contract gives NaN the GPU gives NaN too. (A NaN's sign and
-    payload are the processor's: x86 makes 0 * inf the negative default NaN, the GPU the
-    positive one, so NaN bytes are not compared.)"""
+    """Infinite and NaN fp16 scales, byte for byte, NaN outputs included. A NaN's sign and
+    payload are the processor's: here every NaN comes from an fp16 NaN scale (0x7E00, widened to
+    0x7FC00000 and carried through every later operation) or from 0 * inf (and inf - inf in the
+    sums), which x86, where the oracle runs, makes its default NaN 0xFFC00000. The GPU gives the
+    same bytes in every row. (AArch64, the board's CPU, would make 0 * inf 0x7FC00000: the
+    contract's NaN bytes are the platform's, and this test pins the oracle's.)"""
     rng = np.random.default_rng(91)
     rows, k = 64, 1024
     blocks = C.quantize_q4_0(O.normal_f32((rows, k), 92, 0.02)).reshape(rows, k // 32, 18)
@@ -209,7 +211,9 @@ def test_gemv_nonfinite_scales(gpu):
     nan = np.isnan(want)
     assert nan.any() and np.isinf(want).any()
     assert np.array_equal(np.isnan(got), nan), np.flatnonzero(np.isnan(got) != nan)
-    assert_bytes_equal(got[~nan], want[~nan], "non-NaN outputs")
+    assert want.view(np.uint32)[5] == 0xFFC00000         # 0 * inf
+    assert want.view(np.uint32)[4] == 0x7FC00000         # the NaN scale's own NaN
+    assert_bytes_equal(got, want, "every output, NaN bytes included")
 
 
 def test_gemv_quarters_at_separate_addresses(gpu):
