@@ -71,7 +71,7 @@ hipError_t allow_dynamic_lds(const void *fn, size_t budget) {
 
 size_t argmax_workspace_bytes() { return ARGMAX_KEY_OFFSET + 64; }
 
-M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool argmax, int cus) {
+M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool /*argmax*/, int cus) {
     const int nb = k / QK;
     // Staged activation: int8 values, fp32 scale and int32 sum per block; for
     // X_RMS also the squares of x as float64 and the rmsnorm scale.
@@ -88,7 +88,7 @@ M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool argmax, int cus) {
     //  * Large: bandwidth. Four-wave workgroups, every wave walking tiles
     //    with a stride of the whole grid, at most eight resident waves per CU
     //    (two tiles and the activation column take about 208 VGPRs, two
-    //    waves per SIMD); three workgroups per CU (below).
+    //    waves per SIMD); two workgroups per CU (below).
     // Every workgroup has at least one thread per activation block, so x is
     // staged in one pass. (Spreading an fp32 x's quantization over 2-8
     // threads per block, in helper waves or in the spare threads of the
@@ -101,18 +101,14 @@ M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool argmax, int cus) {
     int grid = (tiles + waves - 1) / waves;
     if (tiles > 2 * cus) {
         if (tiles > 8 * cus) {
-            // Three workgroups per CU: two are resident at a time and the
-            // third takes over as soon as one finishes, which shortened the
-            // LM head by 4% against a grid of exactly the resident
-            // workgroups. Not where a workgroup's start is dear: a late one
-            // pays the rmsnorm's float64 chain (or silu's exponentials) again
-            // on the critical path, and the argmax's last workgroup waits for
-            // every other one's atomics; those keep two.
-            const bool cheap_start = (xf == X_ENGINE || xf == X_Q8_0 || xf == X_F32) && !argmax;
+            // Exactly the resident workgroups: two per CU. A third per CU
+            // (taking over as one finishes) made the LM head slower with
+            // every activation form: 25.8 against 24.4-25.0 us with engine x,
+            // 26.4 against 24.4 with fp32 x, and the decode chain 237.2
+            // against 235.1 us per step.
             waves = 4 > min_waves ? 4 : min_waves;
             grid = (tiles + waves - 1) / waves;
-            const int cap = cus * (cheap_start ? 3 : 2);
-            if (grid > cap) grid = cap;
+            if (grid > 2 * cus) grid = 2 * cus;
         } else {
             const int per_cu = (tiles + cus - 1) / cus;
             waves = (per_cu + MID_TILES_PER_WAVE - 1) / MID_TILES_PER_WAVE;
