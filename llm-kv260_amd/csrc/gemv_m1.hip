@@ -78,8 +78,10 @@ M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool /*argmax*/, int cus) {
     const size_t x_lds = x_lds_bytes(nb) + (xf == X_RMS ? rms_sq_doubles(k) * 8 + 16 : 0);
     // Launch shape, from what bounds each size:
     //  * Small matrices (at most two tiles per CU): latency. One tile per
-    //    wave, workgroups spread over every CU (each stages its own copy of
-    //    x in parallel).
+    //    wave, two-wave workgroups spread over the CUs (each stages its own
+    //    copy of x in parallel). In the decode chain two waves per workgroup
+    //    ran 234.3-235.0 us per step against 235.7-236.0 with one and 244.5
+    //    with four (alone, q|k|v and o are within 0.04 us either way).
     //  * Mid-size (up to eight tiles per CU): one workgroup per CU whose waves
     //    walk MID_TILES_PER_WAVE tiles each. One per wave, every tile in
     //    flight at once: gate|up 5.8 us, against 6.0 at four per wave and
@@ -97,7 +99,7 @@ M1Shape gemv_m1_shape(int tiles, int k, XFormat xf, bool /*argmax*/, int cus) {
     // The rmsnorm forms stage their x with four threads per block where a
     // workgroup can hold them (K = 2048: four waves).
     if (xf == X_RMS && nb / 16 <= MAX_THREADS / 64 && nb / 16 > min_waves) min_waves = nb / 16;
-    int waves = min_waves;
+    int waves = min_waves > 2 ? min_waves : 2;
     int grid = (tiles + waves - 1) / waves;
     if (tiles > 2 * cus) {
         if (tiles > 8 * cus) {
