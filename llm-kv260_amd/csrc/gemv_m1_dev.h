@@ -12,8 +12,8 @@
 //    global_load_dwordx4, lane l loading bytes 1024 p + 16 l of the tile.
 //  * Each wave keeps two tiles in registers: while it computes one, the next
 //    is in flight, and the one it just consumed is refilled before its terms
-//    are computed (18 KB per wave). Large matrices launch three 4-wave
-//    workgroups per CU, two of them resident at a time.
+//    are computed (18 KB per wave). Large matrices launch two 4-wave
+//    workgroups per CU, both resident.
 //  * A tile's pieces go through a per-wave 9 KB LDS slab (ds_write_b128 in
 //    load order, ds_read_b128 in chunk order), so that lane l ends up with
 //    chunk l: 144 bytes, eight whole blocks.
