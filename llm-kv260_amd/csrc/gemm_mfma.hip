@@ -446,10 +446,7 @@ void gemm_mfma_kernel(GemmParams Pm) {
         Kernel<MT, D, P, OCC, NRL, false>::run(Pm, lds);
 }
 
-#ifndef W4A8_GEMM_DEPTH
-#define W4A8_GEMM_DEPTH 2
-#endif
-constexpr int DEPTH = W4A8_GEMM_DEPTH;
+constexpr int DEPTH = 2;
 
 template <int MT, int D, int OCC, int NRL = 16>
 hipError_t launch_geo(const GemmParams &Pm, hipStream_t stream) {
@@ -486,13 +483,10 @@ hipError_t launch_mt(const GemmParams &Pm, hipStream_t stream) {
     return launch_geo<MT, 1, OCC, NRL>(Pm, stream);
 }
 
-#ifndef W4A8_GEMM_OCC
-#define W4A8_GEMM_OCC 2
-#endif
-
-#ifndef W4A8_GEMM_SPLIT_ITEMS
-#define W4A8_GEMM_SPLIT_ITEMS 160
-#endif
+// Workgroups per CU, and the item count under which wide token tiles split
+// into 16-token items (below).
+constexpr int GEMM_OCC = 2;
+constexpr long GEMM_SPLIT_ITEMS = 160;
 
 hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
     // 16, 32 or 64 tokens per item. The widest tile that covers M streams the
@@ -504,11 +498,11 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
     // win at M > 32 only (8.8 against 9.5 us at M = 64; at M = 24 the 32-token
     // tile is faster). A round holds 128 (or, at two workgroups per CU, 64)
     // token-chunks of activations.
-    constexpr int OCC = W4A8_GEMM_OCC;
+    constexpr int OCC = GEMM_OCC;
     const long row_groups = (Pm.rows + NR - 1) / NR;
     int mt = Pm.m <= 16 ? 1 : Pm.m <= 32 ? 2 : 4;
     const long wide_items = row_groups * ((Pm.m + 16 * mt - 1) / (16 * mt));
-    if (mt > 1 && (wide_items < W4A8_GEMM_SPLIT_ITEMS || (mt == 4 && wide_items < 2 * W4A8_GEMM_SPLIT_ITEMS))) mt = 1;
+    if (mt > 1 && (wide_items < GEMM_SPLIT_ITEMS || (mt == 4 && wide_items < 2 * GEMM_SPLIT_ITEMS))) mt = 1;
     // One token group over long rows (K >= 8192: down) with fewer 16-row
     // groups than CUs: 8-row items, eight chunks per round, one workgroup per
     // CU. Down at M = 5..16 takes 9.2-10.1 us against 10.4-10.6 with 16-row
@@ -526,9 +520,7 @@ hipError_t launch_tokens(const GemmParams &Pm, hipStream_t stream) {
 
 // From this many rows on, the row-split kernel: at gate|up (16,384 rows) it is
 // 8-26% faster; at 3,072 rows it was twice as slow (48 workgroups).
-#ifndef W4A8_ROWS_MIN
-#define W4A8_ROWS_MIN 8192
-#endif
+constexpr int ROWS_MIN = 8192;
 
 hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hipStream_t stream) {
     // One token is the M = 1 GEMV, byte for byte by the contract, and faster.
@@ -551,7 +543,7 @@ hipError_t launch_gemm(const MatrixRef &w, const uint8_t *x, int m, float *y, hi
     if ((size_t)P.rows * (size_t)(P.k / QK * Q4_0_BYTES) >= 0x7fff0000u ||
         (size_t)64 * P.rows * 4 >= 0x7fff0000u)
         return hipErrorInvalidValue;
-    const bool by_rows = P.rows >= W4A8_ROWS_MIN && gemm_rows_fits(P.rows, P.k);
+    const bool by_rows = P.rows >= ROWS_MIN && gemm_rows_fits(P.rows, P.k);
     for (int m0 = 0; m0 < m; m0 += 64) {
         P.x = x + (size_t)m0 * P.x_stride;
         P.y = y + (size_t)m0 * P.rows;

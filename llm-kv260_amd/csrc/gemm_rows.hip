@@ -489,13 +489,8 @@ hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y,
     P.k = k;
     P.m = m;
     P.x_stride = k + k / 8;
-#ifndef W4A8_ROWS_PACKED
-#define W4A8_ROWS_PACKED 1
-#endif
-#if W4A8_ROWS_PACKED
     if (m <= 4) return launch_rows_mt<1, 4>(P, stream);
     if (m <= 8) return launch_rows_mt<1, 2>(P, stream);
-#endif
     if (m <= 16) return launch_rows_mt<1>(P, stream);
     if (m <= 32) return launch_rows_mt<2>(P, stream);
     return launch_rows_mt<4>(P, stream);

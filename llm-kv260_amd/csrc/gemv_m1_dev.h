@@ -100,18 +100,9 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
     return v;
 }
 
-#ifndef W4A8_BATCH_WAVES
-#define W4A8_BATCH_WAVES 4
-#endif
-#ifndef W4A8_BATCH_TILES_PER_WAVE
-#define W4A8_BATCH_TILES_PER_WAVE 20
-#endif
-constexpr int BATCH_THREADS = 64 * W4A8_BATCH_WAVES;
-constexpr int BATCH_TILES_PER_WAVE = W4A8_BATCH_TILES_PER_WAVE;
-#ifndef W4A8_MID_TILES_PER_WAVE
-#define W4A8_MID_TILES_PER_WAVE 1
-#endif
-constexpr int MID_TILES_PER_WAVE = W4A8_MID_TILES_PER_WAVE;
+constexpr int BATCH_THREADS = 64 * 4;
+constexpr int BATCH_TILES_PER_WAVE = 20;
+constexpr int MID_TILES_PER_WAVE = 1;
 
 struct BatchEntry {
     const uint8_t *w;

@@ -38,9 +38,6 @@ constexpr int MT_MAX = 8;                        // tokens per launch
 constexpr int MT_THREADS = 512;
 constexpr size_t MT_LDS_BUDGET = 160 * 1024;
 
-#ifndef W4A8_MT_SPLIT
-#define W4A8_MT_SPLIT 1
-#endif
 
 struct MtParams {
     const uint8_t *w;
@@ -389,10 +386,6 @@ bool gemv_mt_fits(int m, int rows, int k) {
 }
 
 int gemv_mt_max_m(int rows, int k) {
-#ifdef W4A8_MT_MAX_ALL
-    (void)rows; (void)k;
-    return W4A8_MT_MAX_ALL;
-#else
     // Measured on MI355X against the MFMA kernels (rotated weights, us, with
     // the v_dot4 block dots):
     //  * m = 2 on every shape (q|k|v 4.3 against 4.9, o 4.2 against 4.8,
@@ -408,13 +401,12 @@ int gemv_mt_max_m(int rows, int k) {
     //    even at m = 5, 6.
     const int rpw = 64 / (k / 256 > 0 ? k / 256 : 1);
     const int tiles = (rows + rpw - 1) / rpw;
-    if (W4A8_MT_SPLIT && tiles <= 4 * device_cu_count()) {
+    if (tiles <= 4 * device_cu_count()) {
         if (k >= 8192) return 8;
         if (k == 2048 && rows >= 8192) return 6;
     }
     if (rows >= 8192 || k >= 4096) return 4;
     return 2;
-#endif
 }
 
 hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, int rows, int k, hipStream_t stream) {
@@ -442,7 +434,7 @@ hipError_t launch_gemv_mt(const uint8_t *w, const uint8_t *x, int m, float *y, i
     //  * more (the LM head): four-wave workgroups striding over the matrix,
     //    two per CU.
     int waves, grid;
-    const bool split = W4A8_MT_SPLIT && P.tiles <= 4 * cus;
+    const bool split = P.tiles <= 4 * cus;
     if (split) {
         // One tile per pair of waves, four pairs per workgroup.
         waves = 8;
