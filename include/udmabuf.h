@@ -18,7 +18,11 @@
  *   - udmabuf_invalidate(p, len): the CPU will read [p, p+len). The parts
  *     not host-current are copied device -> host, synchronously (the device
  *     copy may hold writes made outside the engine calls); host-current parts
- *     need nothing.
+ *     need nothing. A write into the device copy of a host-current range by
+ *     anything but an engine call (a kernel of the caller's own at the pool's
+ *     device address) is therefore not seen by the host; clean such a range
+ *     with 1 MiB or more first (copied at once, it leaves nothing
+ *     host-current), or keep those writes to ranges the host never cleaned.
  * So the reference's discipline ("clean before the engine reads what the CPU
  * wrote, invalidate before the CPU reads what the engine wrote") still carries
  * the data exactly where it did on the board, and its per-call clean of x and

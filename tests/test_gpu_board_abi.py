@@ -260,3 +260,62 @@ def test_gen_vectors_exactness(board, gen_vectors, name):
         got = _v2_check_case(L, pool, blocks, x_eng, rows, k)
         pool.used = 0
         assert_bytes_equal(got, want, f"gen_vectors {name}, gemv2")
+
+
+class _DeviceBytes:
+    """A pool's device bytes at `phys`, for torch.as_tensor (CUDA array interface)."""
+
+    def __init__(self, phys, n):
+        self.__cuda_array_interface__ = {"shape": (n,), "typestr": "|u1", "data": (phys, False), "version": 3}
+
+
+def test_pool_copies_follow_the_current_copy(board):
+    """Which copy of a pool range is current: bytes written into the device copy
+    from outside the engine calls reach the host through invalidate (in a range
+    that is not host-current: a clean of 1 MiB or more copies at once and
+    leaves none); a range the host cleaned is not overwritten by invalidate (its
+    host bytes are the current ones); an engine call's y lands in the host
+    copy, and a later clean of new bytes in that range reaches the next call
+    that reads it."""
+    import torch
+    L, pool = board
+    span = 1 << 20
+    p = L.udmabuf_alloc(ctypes.byref(pool), span, 4096)
+    L.udmabuf_clean(p, span)                          # copied at once: no part host-current
+    n = 4096 + 20                                     # whole 16-byte pieces plus a ragged tail
+    phys = pool.phys + (p - pool.base)
+    host = np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(p))
+    host[:] = 0x11
+    dev_view = torch.as_tensor(_DeviceBytes(phys, n), device="cuda")
+    dev_view.fill_(0x5A)                              # a write the engine calls know nothing of
+    torch.cuda.synchronize()
+    L.udmabuf_invalidate(p, n)
+    assert (host == 0x5A).all()
+    host[:] = 0x33
+    L.udmabuf_clean(p, n)                             # host-current now: nothing copied yet
+    L.udmabuf_invalidate(p, n)
+    assert (host == 0x33).all(), "invalidate overwrote bytes the host had cleaned"
+    # An engine call writes its y into the host copy; that range then takes,
+    # cleaned, the second call's x (576 rows of y = the 2,304 bytes of an
+    # engine-layout x at k = 2048), which the second call must read.
+    k = 2048
+    rows1 = (k + k // 8) // 4
+    blocks, x_eng, want = _case(rows1, k, 77)
+    _, wp = _alloc(L, pool, blocks.reshape(-1), 64 << 10)
+    _, xp = _alloc(L, pool, x_eng)
+    y_host, yp = _poisoned_y(L, pool, rows1)
+    d = Dev()
+    assert L.gemv_dev_open(ctypes.byref(d)) == 0
+    L.gemv_dev_run(ctypes.byref(d), wp, xp, yp, k, rows1)
+    assert_bytes_equal(_read_y(L, y_host, rows1), want, "first call")
+    rows2 = 64
+    blocks2, x2, want2 = _case(rows2, k, 78)
+    assert len(x2) == 4 * rows1
+    _, wp2 = _alloc(L, pool, blocks2.reshape(-1), 64 << 10)
+    y2_host, yp2 = _poisoned_y(L, pool, rows2)
+    ctypes.memmove(y_host, np.ascontiguousarray(x2).ctypes.data, len(x2))
+    L.udmabuf_clean(y_host, len(x2))
+    L.gemv_dev_run(ctypes.byref(d), wp2, yp, yp2, k, rows2)
+    assert_bytes_equal(_read_y(L, y2_host, rows2), want2, "second call, x where the first call's y was")
+    L.gemv_dev_close(ctypes.byref(d))
+    pool.used = 0
