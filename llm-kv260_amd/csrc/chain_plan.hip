@@ -43,7 +43,15 @@ struct w4a8_chain_plan {
     int n = 0;
     std::vector<int> kind;                 // kernel variant per step
     std::vector<uint32_t> grid, threads, group;
-    char *kargs = nullptr;                 // pinned host memory, ARG_STRIDE bytes per step
+    // The steps' argument blocks, ARG_STRIDE bytes each: in device memory
+    // (what the packets point at) and a host copy (the timed launch builds
+    // its blocks from it). In pinned coherent host memory instead, every
+    // launch paid about 50 us more: its first packet's acquire drops the
+    // blocks from the caches, and each of the first pass's 65 dispatches then
+    // fetched its block across PCIe (one pass 296 us against 244-248; the
+    // steady state the same, 233-234 us per pass).
+    char *kargs = nullptr;
+    std::vector<char> kargs_host;
     hsa_signal_t done{};                   // launches in flight
     char *timed_kargs = nullptr;           // the timed launch's, device memory: one block per dispatch
     size_t timed_bytes = 0;
@@ -378,17 +386,18 @@ int chain_plan_create(const w4a8_plan_step *steps, int n, bool overlapped, w4a8_
             std::memcpy(host.data() + (size_t)j * ARG_STRIDE + sizeof(PlanArgs), &S, sizeof S);
         }
     }
-    hipError_t e = hipHostMalloc(&p->kargs, host.size(), hipHostMallocCoherent);
-    if (e == hipSuccess) std::memcpy(p->kargs, host.data(), host.size());
+    hipError_t e = hipMalloc(&p->kargs, host.size());
+    if (e == hipSuccess) e = hipMemcpy(p->kargs, host.data(), host.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
-        if (p->kargs) (void)hipHostFree(p->kargs);
+        if (p->kargs) (void)hipFree(p->kargs);
         if (p->flags) (void)hipFree(p->flags);
         delete p;
         he = e;
         return W4A8_ERR_HIP;
     }
+    p->kargs_host = std::move(host);
     if (hsa_signal_create(0, 0, nullptr, &p->done) != HSA_STATUS_SUCCESS) {
-        (void)hipHostFree(p->kargs);
+        (void)hipFree(p->kargs);
         if (p->flags) (void)hipFree(p->flags);
         delete p;
         return W4A8_ERR_HSA;
@@ -506,7 +515,7 @@ int chain_plan_launch_timed(w4a8_chain_plan *p, int passes, unsigned long long *
     for (size_t i = 0; i < total; ++i) {
         char *a = host.data() + i * ARG_STRIDE;
         const size_t j = i % (size_t)p->n;
-        std::memcpy(a, p->kargs + j * ARG_STRIDE, sizeof(PlanArgs));
+        std::memcpy(a, p->kargs_host.data() + j * ARG_STRIDE, sizeof(PlanArgs));
         unsigned long long *st = stamps + 2 * slot;
         std::memcpy(a + sizeof(PlanArgs), &st, sizeof st);
         slot += p->grid[j];
@@ -544,7 +553,7 @@ int chain_plan_destroy(w4a8_chain_plan *p) {
     const int s = chain_plan_wait(p, 10000);
     if (s != W4A8_OK) return s;   // work in flight: the plan stays valid
     hsa_signal_destroy(p->done);
-    (void)hipHostFree(p->kargs);
+    (void)hipFree(p->kargs);
     if (p->timed_kargs) (void)hipFree(p->timed_kargs);
     if (p->flags) (void)hipFree(p->flags);
     delete p;
