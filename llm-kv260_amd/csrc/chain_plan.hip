@@ -15,10 +15,9 @@
 // an output that a later step reads is written through to the device's
 // coherence point and waited for before its waves end, and that step reads
 // it from there (the kernels' _yc / _xc variants); everything else goes
-// through the caches as before. The kernel arguments sit in pinned,
-// coherent host memory, written once when the plan is made (as fast as
-// device memory here, 243-244 against 243 us per step, and readable by
-// tools that inspect a dispatch's arguments from the host).
+// through the caches as before. The kernel arguments sit in device memory,
+// written once when the plan is made (w4a8_chain_plan says why not in host
+// memory).
 //
 // This mirrors how the reference drives its engine: the host starts the
 // work and later waits for it (board/kv260gemv/gemv2_dev.h:40-44,
