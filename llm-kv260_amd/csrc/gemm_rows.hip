@@ -8,7 +8,8 @@
 // b % 8 from +0.0f. At the end the pair meets once: wave 0's
 // (a0 + a1) + (a2 + a3) plus wave 1's (a4 + a5) + (a6 + a7) is the
 // adjacent-pair tree's last add. A workgroup holds two or four pairs (32 or
-// 64 rows, pairs_of), so every wave has the same work.
+// 64 rows, pairs_of), so every wave has the same work. From 17 tokens the
+// group has four waves instead (QuadKernel), each owning two accumulators.
 //
 // K goes by segments of 512 values (16 blocks). Per segment a pair stages its
 // 16 rows' 288-byte runs in a slab of its own, and the workgroup stages the
@@ -455,6 +456,279 @@ struct RowsKernel {
     }
 };
 
+// Four waves per 16-row group (a quad): wave q owns the contract's
+// accumulators 2q and 2q + 1, so it takes the blocks b with b % 8 in
+// {2q, 2q + 1}, in increasing b. A workgroup holds GROUPS groups (64 rows
+// at four: 16 waves), sharing the staged activation as the pairs do, and a
+// SIMD then runs four waves instead of two: one wave's LDS reads, MFMA
+// latency and waits are covered by the others' fp32 terms. At the end wave
+// 0 of the group adds the tree: (p0 + p1) + (p2 + p3), p_q = a_2q + a_2q+1,
+// the other waves' parts through LDS (over the activation buffers, which
+// every wave has finished reading by then).
+template <int MT, int GROUPS>
+struct QuadGeo {
+    static constexpr int TT = 16 * MT;
+    static constexpr int APITCH = SEG + 16;
+    static constexpr int XDP = TT + 4;
+    static constexpr int XD_OFF = TT * APITCH;
+    static constexpr int XBUF = XD_OFF + SEG_BLOCKS * XDP * 4;
+    static constexpr int THREADS = 64 * 4 * GROUPS;
+    static constexpr int SLAB_OFF = 2 * XBUF;                       // [2][GROUPS] slabs
+    static constexpr int LDS = SLAB_OFF + 2 * GROUPS * SLAB;
+    static constexpr int EX_FLOATS = GROUPS * 3 * TT * 16;         // the parts of waves 1..3
+    static_assert(EX_FLOATS * 4 <= LDS, "exchange within the buffers");
+    static_assert(LDS <= LDS_MAX, "LDS budget");
+    static constexpr int X_PIECES = TT * (SEG / 16);
+    static constexpr int D_PIECES = TT * (SEG_BLOCKS / 4);
+    static constexpr int SX = (X_PIECES + THREADS - 1) / THREADS;
+    static constexpr int SD = (D_PIECES + THREADS - 1) / THREADS;
+    static constexpr int SWQ = (W_PIECES + 255) / 256;               // weight pieces per thread of a group
+};
+
+template <int MT, int GROUPS>
+struct QuadKernel {
+    using G = QuadGeo<MT, GROUPS>;
+
+    struct Regs {
+        u32x4 w[G::SWQ];
+        u32x4 x[G::SX];
+        u32x4 d[G::SD];
+    };
+    struct Slots {
+        uint32_t w_go[G::SWQ];
+        int w_lo[G::SWQ];
+        uint32_t x_go[G::SX];
+        int x_lo[G::SX];
+        uint32_t d_go[G::SD];
+        int d_lo[G::SD];
+    };
+
+    static __device__ __forceinline__ void slots(const RowsParams &P, int row_bytes, Slots &s) {
+        const int tid = threadIdx.x;
+        const int tp = tid & 255;                // thread within the group
+#pragma unroll
+        for (int i = 0; i < G::SWQ; ++i) {
+            const int n = tp + 256 * i;
+            const int r = n / 18, q = n - 18 * (n / 18);
+            const bool has = n < W_PIECES;
+            s.w_go[i] = has ? (uint32_t)r * (uint32_t)row_bytes + 16u * (uint32_t)q : (uint32_t)OUT_OF_RANGE;
+            s.w_lo[i] = has ? r * WPITCH + 16 * q : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i) {
+            const int n = tid + G::THREADS * i;
+            const int t = n / 32, p = n - 32 * t;
+            const bool has = n < G::X_PIECES;
+            s.x_go[i] = has ? (uint32_t)t * (uint32_t)P.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.x_lo[i] = has ? t * G::APITCH + 16 * p : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i) {
+            const int n = tid + G::THREADS * i;
+            const int p = n / G::TT, t = n - G::TT * p;
+            const bool has = n < G::D_PIECES;
+            s.d_go[i] = has ? (uint32_t)t * (uint32_t)P.x_stride + 16u * (uint32_t)p : (uint32_t)OUT_OF_RANGE;
+            s.d_lo[i] = has ? G::XD_OFF / 4 + 4 * p * G::XDP + t : -1;
+        }
+    }
+
+    static __device__ __forceinline__ void load(const RowsParams &P, const Slots &s, int row_bytes, int n0, int sg,
+                                                int nseg, Regs &rg) {
+        const bool live = sg < nseg;
+        const uint32_t rows_left = n0 < P.rows ? (uint32_t)(P.rows - n0) : 0u;
+        const uint32_t w_skip = (uint32_t)sg * SEG_ROW_BYTES;
+        const __amdgpu_buffer_rsrc_t wb =
+            rsrc(P.w + (size_t)n0 * row_bytes + (live ? w_skip : 0u),
+                 live && rows_left ? rows_left * (uint32_t)row_bytes - w_skip : 0u);
+        const uint32_t xs = (uint32_t)P.m * (uint32_t)P.x_stride;
+        const __amdgpu_buffer_rsrc_t xb = rsrc(P.x + (live ? sg * SEG : 0), live ? xs - (uint32_t)(sg * SEG) : 0u);
+        const uint32_t d0 = (uint32_t)P.k + (uint32_t)sg * SEG_BLOCKS * 4u;
+        const __amdgpu_buffer_rsrc_t db = rsrc(P.x + (live ? d0 : 0u), live ? xs - d0 : 0u);
+#pragma unroll
+        for (int i = 0; i < G::SWQ; ++i) rg.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wb, (int)s.w_go[i], 0, CACHE_NT);
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i) rg.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xb, (int)s.x_go[i], 0, 0);
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i) rg.d[i] = __builtin_amdgcn_raw_buffer_load_b128(db, (int)s.d_go[i], 0, 0);
+    }
+
+    static __device__ __forceinline__ void stage(uint8_t *xbuf, uint8_t *slab, const Slots &s, const Regs &rg) {
+#pragma unroll
+        for (int i = 0; i < G::SWQ; ++i)
+            if (s.w_lo[i] >= 0) *reinterpret_cast<u32x4 *>(slab + s.w_lo[i]) = rg.w[i];
+#pragma unroll
+        for (int i = 0; i < G::SX; ++i)
+            if ((i + 1) * G::THREADS <= G::X_PIECES || s.x_lo[i] >= 0)
+                *reinterpret_cast<u32x4 *>(xbuf + s.x_lo[i]) = rg.x[i];
+#pragma unroll
+        for (int i = 0; i < G::SD; ++i)
+            if ((i + 1) * G::THREADS <= G::D_PIECES || s.d_lo[i] >= 0) {
+                uint32_t *xd = reinterpret_cast<uint32_t *>(xbuf) + s.d_lo[i];
+                const u32x4 v = rg.d[i];
+                xd[0] = v.x;
+                xd[G::XDP] = v.y;
+                xd[2 * G::XDP] = v.z;
+                xd[3 * G::XDP] = v.w;
+            }
+    }
+
+    // Block B of the wave's view of the segment (the wave's blocks start at
+    // 2q, folded into the pointers; B keeps the parity, which fixes where the
+    // block's scale and nibbles sit in its dwords): its MFMA sums for every
+    // token tile, the weight scale and the tokens' scales.
+    template <int B>
+    static __device__ __forceinline__ void block_sums(const uint8_t *slab, const uint8_t *xq, const float *xd, int j,
+                                                      int g, v4i v[MT], float &dw, float dx[MT]) {
+        long bw;
+        RowsKernel<MT>::template weights_of<B>(slab, j, g, bw, dw);
+        const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
+        const uint8_t *xa = xq + j * G::APITCH + 32 * B + 8 * g;
+        const float *xs = xd + B * G::XDP + 4 * g + (j & 3);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
+            dx[t] = xs[16 * t];
+            v4i z = {0, 0, 0, 0};
+            z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+            v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
+        }
+    }
+
+    // Block B (accumulator c of the wave's two): MFMAs first, then the fp32
+    // terms.
+    template <int B, int C>
+    static __device__ __forceinline__ void one_block(const uint8_t *slab, const uint8_t *xq, const float *xd, int j,
+                                                     int g, float acc[2][MT][4]) {
+        v4i v[MT];
+        float dw, dx[MT];
+        block_sums<B>(slab, xq, xd, j, g, v, dw, dx);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const float dxs[4] = {bcast<0>(dx[t]), bcast<1>(dx[t]), bcast<2>(dx[t]), bcast<3>(dx[t])};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float a = (float)v[t][r] * dw;
+                acc[C][t][r] = acc[C][t][r] + a * dxs[r];
+            }
+        }
+    }
+    // Blocks B0 (accumulator 2q) and B0 + 1 (accumulator 2q + 1), in order.
+    template <int B0>
+    static __device__ __forceinline__ void two_blocks(const uint8_t *slab, const uint8_t *xq, const float *xd, int j,
+                                                      int g, float acc[2][MT][4]) {
+        one_block<B0, 0>(slab, xq, xd, j, g, acc);
+        // Keep each block's MFMAs beside its terms: hoisted together, the
+        // four blocks' results would not fit the 128 registers a wave has
+        // at four waves per SIMD.
+        __builtin_amdgcn_sched_barrier(0);
+        one_block<B0 + 1, 1>(slab, xq, xd, j, g, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    static __device__ __forceinline__ void run(const RowsParams &P, uint8_t *lds) {
+        const int tid = threadIdx.x;
+        const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int grp = wave >> 2, q = wave & 3;
+        const int j = lane & 15, g = lane >> 4;
+        const int row_bytes = P.k / QK * Q4_0_BYTES;
+        const int nseg = P.k / SEG;
+        const int n0 = ((int)blockIdx.x * GROUPS + grp) * 16;
+
+        Slots s;
+        slots(P, row_bytes, s);
+        Regs rg;
+        load(P, s, row_bytes, n0, 0, nseg, rg);
+        stage(lds, lds + G::SLAB_OFF + grp * SLAB, s, rg);
+        load(P, s, row_bytes, n0, 1, nseg, rg);
+        __syncthreads();
+
+        float acc[2][MT][4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[c][t][r] = 0.0f;
+
+        for (int sg = 0; sg < nseg; ++sg) {
+            const uint8_t *xbuf = lds + (sg & 1) * G::XBUF;
+            const uint8_t *slab = lds + G::SLAB_OFF + ((sg & 1) * GROUPS + grp) * SLAB + 36 * q;
+            const uint8_t *xq = xbuf + 64 * q;
+            const float *xd = reinterpret_cast<const float *>(xbuf + G::XD_OFF) + 2 * q * G::XDP;
+            two_blocks<0>(slab, xq, xd, j, g, acc);
+            two_blocks<8>(slab, xq, xd, j, g, acc);
+            // The terms are complete here: left alone, the compiler sinks
+            // them below the staging's divergent stores, and the DPP
+            // broadcasts of the scales then no longer fold into their
+            // multiplies.
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) __asm__ volatile("" : "+v"(acc[c][t][r]));
+            // Segment sg + 1 into the other buffers (last read for segment
+            // sg - 1, before the previous barrier); the registers then take
+            // segment sg + 2.
+            const int nx = sg + 1;
+            stage(lds + (nx & 1) * G::XBUF, lds + G::SLAB_OFF + ((nx & 1) * GROUPS + grp) * SLAB, s, rg);
+            load(P, s, row_bytes, n0, nx + 1, nseg, rg);
+            __syncthreads();
+        }
+
+        // The tree: waves 1..3 hand their parts to wave 0.
+        float part[MT][4];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[t][r] = acc[0][t][r] + acc[1][t][r];
+        float *ex = reinterpret_cast<float *>(lds) + grp * 3 * G::TT * 16;
+        if (q != 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ex[((q - 1) * G::TT + 16 * t + 4 * g + r) * 16 + j] = part[t][r];
+        }
+        __syncthreads();
+        if (q == 0) {
+            const uint32_t y_bytes = (uint32_t)P.m * (uint32_t)P.rows * 4u;
+            const __amdgpu_buffer_rsrc_t yb = rsrc(P.y, y_bytes);
+            const bool row_ok = n0 + j < P.rows;
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tok = 16 * t + 4 * g + r;
+                    const float p1 = ex[(0 * G::TT + tok) * 16 + j];
+                    const float p2 = ex[(1 * G::TT + tok) * 16 + j];
+                    const float p3 = ex[(2 * G::TT + tok) * 16 + j];
+                    const float yv = (part[t][r] + p1) + (p2 + p3);
+                    const bool ok = row_ok && tok < P.m;
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(yv), yb, ok ? (int)(((uint32_t)tok * (uint32_t)P.rows + (uint32_t)(n0 + j)) * 4u) : OUT_OF_RANGE,
+                        0, 0);
+                }
+        }
+    }
+};
+
+template <int MT, int GROUPS>
+__global__ __launch_bounds__(64 * 4 * GROUPS) void gemm_rows_quad_kernel(RowsParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    QuadKernel<MT, GROUPS>::run(P, lds);
+}
+
+template <int MT, int GROUPS>
+hipError_t launch_rows_quad(const RowsParams &P, hipStream_t stream) {
+    const void *fn = reinterpret_cast<const void *>(&gemm_rows_quad_kernel<MT, GROUPS>);
+    const hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
+    if (e != hipSuccess) return e;
+    using G = QuadGeo<MT, GROUPS>;
+    const int grid = (P.rows + 16 * GROUPS - 1) / (16 * GROUPS);
+    hipLaunchKernelGGL((gemm_rows_quad_kernel<MT, GROUPS>), dim3((unsigned)grid), dim3(G::THREADS), G::LDS, stream, P);
+    return hipGetLastError();
+}
+
 template <int MT, int PK>
 __global__ __launch_bounds__(64 * 2 * pairs_of<MT>()) void gemm_rows_kernel(RowsParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -492,8 +766,8 @@ hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y,
     if (m <= 4) return launch_rows_mt<1, 4>(P, stream);
     if (m <= 8) return launch_rows_mt<1, 2>(P, stream);
     if (m <= 16) return launch_rows_mt<1>(P, stream);
-    if (m <= 32) return launch_rows_mt<2>(P, stream);
-    return launch_rows_mt<4>(P, stream);
+    if (m <= 32) return launch_rows_quad<2, 4>(P, stream);
+    return launch_rows_quad<4, 4>(P, stream);
 }
 
 }  // namespace w4a8
