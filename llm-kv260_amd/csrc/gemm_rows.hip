@@ -18,7 +18,8 @@
 //
 // The integer part is v_mfma_i32_16x16x32_i8 as in gemm_mfma.hip (K = 32 is
 // one block; unsigned nibbles, then a second MFMA against a constant -8
-// operand). Operand layout of the 16x16x32 i8 MFMA (64 lanes):
+// operand; at four token tiles the weights made signed once instead,
+// signed_nibbles). Operand layout of the 16x16x32 i8 MFMA (64 lanes):
 //   A: lane l holds A[i = l % 16][k = 8 (l / 16) .. + 7]      (token i)
 //   B: lane l holds B[k = 8 (l / 16) .. + 7][j = l % 16]      (row j)
 //   D: lane l holds D[i = 4 (l / 16) + r][j = l % 16], r = 0..3
@@ -61,6 +62,19 @@ __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long
 template <int R>
 __device__ __forceinline__ float bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), R * 0x55, 0xF, 0xF, true));
+}
+
+// Four nibble values n (one a byte, 0..15) as the signed bytes n - 8: n ^ 8
+// is n - 8 as a 4-bit two's-complement number, and its sign (bit 3) spread
+// over the byte's high nibble makes it the 8-bit one. The spread is a
+// multiply by 30 (8 * 30 = 240 = 0xF0) in two 16-bit halves, whose high
+// bytes never carry into each other.
+__device__ __forceinline__ uint32_t signed_nibbles(uint32_t n) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t x = n ^ 0x08080808u;
+    const uint32_t s = x & 0x08080808u;
+    const u16x2 r = __builtin_bit_cast(u16x2, s) * (u16x2){30, 30} + __builtin_bit_cast(u16x2, x);
+    return __builtin_bit_cast(uint32_t, r);
 }
 
 struct RowsParams {
@@ -581,16 +595,30 @@ struct QuadKernel {
                                                       int g, v4i v[MT], float &dw, float dx[MT]) {
         long bw;
         RowsKernel<MT>::template weights_of<B>(slab, j, g, bw, dw);
-        const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
         const uint8_t *xa = xq + j * G::APITCH + 32 * B + 8 * g;
         const float *xs = xd + B * G::XDP + 4 * g + (j & 3);
+        if constexpr (MT >= 4) {
+            // Four token tiles share the weight operand: make it the signed
+            // weights n - 8 once (three integer ops a dword) instead of a
+            // second MFMA per tile against -8.
+            const long sw = as_long(signed_nibbles((uint32_t)bw), signed_nibbles((uint32_t)((unsigned long)bw >> 32)));
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
-            dx[t] = xs[16 * t];
-            v4i z = {0, 0, 0, 0};
-            z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
-            v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
+            for (int t = 0; t < MT; ++t) {
+                const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
+                dx[t] = xs[16 * t];
+                v4i z = {0, 0, 0, 0};
+                v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, sw, z, 0, 0, 0);
+            }
+        } else {
+            const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
+                dx[t] = xs[16 * t];
+                v4i z = {0, 0, 0, 0};
+                z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+                v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
+            }
         }
     }
 
