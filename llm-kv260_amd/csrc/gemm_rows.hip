@@ -8,7 +8,7 @@
 // b % 8 from +0.0f. At the end the pair meets once: wave 0's
 // (a0 + a1) + (a2 + a3) plus wave 1's (a4 + a5) + (a6 + a7) is the
 // adjacent-pair tree's last add. A workgroup holds two or four pairs (32 or
-// 64 rows, pairs_of), so every wave has the same work. From 17 tokens the
+// 64 rows, pairs_of), so every wave has the same work. From 5 tokens the
 // group has four waves instead (QuadKernel), each owning two accumulators.
 //
 // K goes by segments of 512 values (16 blocks). Per segment a pair stages its
@@ -499,9 +499,10 @@ struct QuadGeo {
     static constexpr int SWQ = (W_PIECES + 255) / 256;               // weight pieces per thread of a group
 };
 
-template <int MT, int GROUPS>
+template <int MT, int GROUPS, int PK = 1>
 struct QuadKernel {
     using G = QuadGeo<MT, GROUPS>;
+    static_assert(PK == 1 || (PK == 2 && MT == 1), "packed quads: two blocks of at most 8 tokens a tile");
 
     struct Regs {
         u32x4 w[G::SWQ];
@@ -653,7 +654,108 @@ struct QuadKernel {
         __builtin_amdgcn_sched_barrier(0);
     }
 
+    // PK = 2 (at most 8 tokens): blocks B0 and B0 + 1 share one MFMA result
+    // tile, as in the pair kernel's packed_group: the A operand's row i is
+    // (block i / 8, token i % 8), each block's MFMA sees zeros in the other
+    // block's rows, and one MFMA against -8 serves both. Lane l then holds
+    // block B0 + (l / 32) of its row l % 16 for tokens 4 ((l / 16) % 2) + r,
+    // every value live: its accumulator is that block's (2q or 2q + 1).
+    template <int B0>
+    static __device__ __forceinline__ void packed_two(const uint8_t *slab, const uint8_t *xq, const float *xd, int j,
+                                                      int g, float pacc[4]) {
+        const int ablk = j >> 3, atok = j & 7;           // this lane's A row
+        const int dblk = g >> 1, dtok = 4 * (g & 1);     // its result rows
+        const long ax = *reinterpret_cast<const long *>(xq + atok * G::APITCH + 32 * (B0 + ablk) + 8 * g);
+        long bw0, bw1;
+        float dw0, dw1;
+        RowsKernel<MT>::template weights_of<B0>(slab, j, g, bw0, dw0);
+        RowsKernel<MT>::template weights_of<B0 + 1>(slab, j, g, bw1, dw1);
+        v4i d = {0, 0, 0, 0};
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ablk == 0 ? ax : 0L, bw0, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ablk == 1 ? ax : 0L, bw1, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, as_long(0xF8F8F8F8u, 0xF8F8F8F8u), d, 0, 0, 0);
+        const float dw = dblk == 0 ? dw0 : dw1;
+        const float4 dx = *reinterpret_cast<const float4 *>(xd + (B0 + dblk) * G::XDP + dtok);
+        const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float a = (float)d[r] * dw;
+            pacc[r] = pacc[r] + a * dxs[r];
+        }
+    }
+
     static __device__ __forceinline__ void run(const RowsParams &P, uint8_t *lds) {
+        if constexpr (PK == 2)
+            run_packed(P, lds);
+        else
+            run_tiles(P, lds);
+    }
+
+    static __device__ __forceinline__ void run_packed(const RowsParams &P, uint8_t *lds) {
+        const int tid = threadIdx.x;
+        const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int grp = wave >> 2, q = wave & 3;
+        const int j = lane & 15, g = lane >> 4;
+        const int row_bytes = P.k / QK * Q4_0_BYTES;
+        const int nseg = P.k / SEG;
+        const int n0 = ((int)blockIdx.x * GROUPS + grp) * 16;
+
+        Slots s;
+        slots(P, row_bytes, s);
+        Regs rg;
+        load(P, s, row_bytes, n0, 0, nseg, rg);
+        stage(lds, lds + G::SLAB_OFF + grp * SLAB, s, rg);
+        load(P, s, row_bytes, n0, 1, nseg, rg);
+        __syncthreads();
+
+        float pacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int sg = 0; sg < nseg; ++sg) {
+            const uint8_t *xbuf = lds + (sg & 1) * G::XBUF;
+            const uint8_t *slab = lds + G::SLAB_OFF + ((sg & 1) * GROUPS + grp) * SLAB + 36 * q;
+            const uint8_t *xq = xbuf + 64 * q;
+            const float *xd = reinterpret_cast<const float *>(xbuf + G::XD_OFF) + 2 * q * G::XDP;
+            packed_two<0>(slab, xq, xd, j, g, pacc);
+            packed_two<8>(slab, xq, xd, j, g, pacc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) __asm__ volatile("" : "+v"(pacc[r]));
+            const int nx = sg + 1;
+            stage(lds + (nx & 1) * G::XBUF, lds + G::SLAB_OFF + ((nx & 1) * GROUPS + grp) * SLAB, s, rg);
+            load(P, s, row_bytes, n0, nx + 1, nseg, rg);
+            __syncthreads();
+        }
+
+        // a_2q + a_2q+1 meet across the lane halves; then the waves as below.
+        const int dtok = 4 * (g & 1);
+        const bool holder = g < 2;
+        float part[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[r] = pacc[r] + __shfl_xor(pacc[r], 32);
+        float *ex = reinterpret_cast<float *>(lds) + grp * 3 * G::TT * 16;
+        if (q != 0 && holder) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ex[((q - 1) * G::TT + dtok + r) * 16 + j] = part[r];
+        }
+        __syncthreads();
+        if (q == 0) {
+            const uint32_t y_bytes = (uint32_t)P.m * (uint32_t)P.rows * 4u;
+            const __amdgpu_buffer_rsrc_t yb = rsrc(P.y, y_bytes);
+            const bool row_ok = holder && n0 + j < P.rows;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = dtok + r;
+                const float p1 = ex[(0 * G::TT + tok) * 16 + j];
+                const float p2 = ex[(1 * G::TT + tok) * 16 + j];
+                const float p3 = ex[(2 * G::TT + tok) * 16 + j];
+                const float yv = (part[r] + p1) + (p2 + p3);
+                const bool ok = row_ok && tok < P.m;
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __float_as_uint(yv), yb, ok ? (int)(((uint32_t)tok * (uint32_t)P.rows + (uint32_t)(n0 + j)) * 4u) : OUT_OF_RANGE,
+                    0, 0);
+            }
+        }
+    }
+
+    static __device__ __forceinline__ void run_tiles(const RowsParams &P, uint8_t *lds) {
         const int tid = threadIdx.x;
         const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int grp = wave >> 2, q = wave & 3;
@@ -740,20 +842,21 @@ struct QuadKernel {
     }
 };
 
-template <int MT, int GROUPS>
+template <int MT, int GROUPS, int PK>
 __global__ __launch_bounds__(64 * 4 * GROUPS) void gemm_rows_quad_kernel(RowsParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    QuadKernel<MT, GROUPS>::run(P, lds);
+    QuadKernel<MT, GROUPS, PK>::run(P, lds);
 }
 
-template <int MT, int GROUPS>
+template <int MT, int GROUPS, int PK = 1>
 hipError_t launch_rows_quad(const RowsParams &P, hipStream_t stream) {
-    const void *fn = reinterpret_cast<const void *>(&gemm_rows_quad_kernel<MT, GROUPS>);
+    const void *fn = reinterpret_cast<const void *>(&gemm_rows_quad_kernel<MT, GROUPS, PK>);
     const hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
     if (e != hipSuccess) return e;
     using G = QuadGeo<MT, GROUPS>;
     const int grid = (P.rows + 16 * GROUPS - 1) / (16 * GROUPS);
-    hipLaunchKernelGGL((gemm_rows_quad_kernel<MT, GROUPS>), dim3((unsigned)grid), dim3(G::THREADS), G::LDS, stream, P);
+    hipLaunchKernelGGL((gemm_rows_quad_kernel<MT, GROUPS, PK>), dim3((unsigned)grid), dim3(G::THREADS), G::LDS, stream,
+                       P);
     return hipGetLastError();
 }
 
@@ -792,8 +895,11 @@ hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y,
     P.m = m;
     P.x_stride = k + k / 8;
     if (m <= 4) return launch_rows_mt<1, 4>(P, stream);
-    if (m <= 8) return launch_rows_mt<1, 2>(P, stream);
-    if (m <= 16) return launch_rows_mt<1>(P, stream);
+    // One token tile: two 16-row groups a workgroup, two workgroups a CU
+    // (four groups a workgroup were slower: gate|up at 8 / 16 tokens 8.8
+    // against 8.3 / 8.4 us, the LM head 48.2 / 51.7 against 43.6 / 49.5).
+    if (m <= 8) return launch_rows_quad<1, 2, 2>(P, stream);
+    if (m <= 16) return launch_rows_quad<1, 2>(P, stream);
     if (m <= 32) return launch_rows_quad<2, 4>(P, stream);
     return launch_rows_quad<4, 4>(P, stream);
 }
