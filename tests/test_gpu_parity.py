@@ -216,6 +216,33 @@ def test_gemv_nonfinite_scales(gpu):
     assert_bytes_equal(got, want, "every output, NaN bytes included")
 
 
+@pytest.mark.parametrize("m,rows", [(8, 8200), (16, 8200), (24, 8200), (64, 8200), (4, 8200), (3, 2000),
+                                    (24, 2000)])
+def test_gemm_nonfinite_scales(gpu, m, rows):
+    """The M > 1 kernels with infinite and NaN fp16 scales, byte for byte, NaN outputs
+    included: the row-split kernels at every token tiling (8,200 rows: packed block pairs,
+    one, two and four token tiles), the few-token GEMV and the class-split kernel (2,000
+    rows)."""
+    rng = np.random.default_rng(190 + m)
+    k = 1024
+    blocks = C.quantize_q4_0(O.normal_f32((rows, k), 191, 0.02)).reshape(rows, k // 32, 18)
+    specials = np.array([np.inf, -np.inf, np.nan, 65504.0], np.float16)
+    for r in range(0, rows, 37):                     # every 37th row gets one special scale
+        blocks[r, rng.integers(0, k // 32), :2] = specials[(r // 37) % 4:(r // 37) % 4 + 1].view(np.uint8)
+    blocks[5, :, 2:] = 0x88                           # weights all 8 - 8 = 0 ...
+    blocks[5, 3, :2] = np.array([np.inf], np.float16).view(np.uint8)   # ... so 0 * inf: NaN
+    blocks = blocks.reshape(rows, -1)
+    xq, xd = C.quantize_q8_0_rows(O.normal_f32((m, k), 192 + m))
+    xd = xd.copy()
+    xd[m // 2, 7] = np.float16(np.inf)               # an infinite activation scale too
+    want = C.gemm_q4_0_rows(blocks, k, xq, xd)
+    assert np.isnan(want).any() and np.isinf(want).any()
+    x_rows = np.stack([C.pack_x_for_engine(xq[i], xd[i]) for i in range(m)])
+    y = poisoned_f32((m, rows))
+    gpu.gemm_engine(dev(blocks), k, dev(x_rows), out=y)
+    assert_bytes_equal(host(y), want, "gemm, non-finite scales, NaN bytes included")
+
+
 def test_gemv_quarters_at_separate_addresses(gpu):
     """The v1 engine's layout (gemv_dev_start4): four quarters anywhere in memory."""
     import torch
