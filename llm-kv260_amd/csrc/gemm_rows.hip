@@ -363,9 +363,10 @@ struct PairKernel {
 
 // From 5 tokens: four waves per 16-row group (a quad), wave q owning the
 // accumulators 2q and 2q + 1, so it takes the blocks b with b % 8 in
-// {2q, 2q + 1}. At the end wave 0 of the group adds the tree:
-// (p0 + p1) + (p2 + p3), p_q = a_2q + a_2q+1, the other waves' parts through
-// LDS. PK = 2 (at most 8 tokens): packed tiles of two blocks (run_packed).
+// {2q, 2q + 1}. At the end the tree's last adds, (p0 + p1) + (p2 + p3) with
+// p_q = a_2q + a_2q+1, meet through LDS: wave 0 of the group adds them, or
+// at four token tiles wave q adds tile q's. PK = 2 (at most 8 tokens):
+// packed tiles of two blocks.
 template <int MT, int GROUPS, int PK = 1>
 struct QuadKernel {
     using G = Geo<MT, GROUPS, 4>;
@@ -524,6 +525,29 @@ struct QuadKernel {
             __syncthreads();
         }
 
+        if constexpr (MT == 4) {
+            // Every wave hands its four tiles' parts over, and wave q adds
+            // tile q's: the final adds and the stores spread over the group.
+            static_assert(GROUPS * 4 * G::TT * 16 * 4 <= G::LDS, "the exchange within the buffers");
+            float *ex4 = reinterpret_cast<float *>(lds) + grp * 4 * G::TT * 16;
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    ex4[(q * G::TT + 16 * t + 4 * g + r) * 16 + j] = acc[0][t][r] + acc[1][t][r];
+            __syncthreads();
+            const bool row_ok = n0 + j < P.rows;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 16 * q + 4 * g + r;
+                const float p0 = ex4[(0 * G::TT + tok) * 16 + j];
+                const float p1 = ex4[(1 * G::TT + tok) * 16 + j];
+                const float p2 = ex4[(2 * G::TT + tok) * 16 + j];
+                const float p3 = ex4[(3 * G::TT + tok) * 16 + j];
+                store_y(P, row_ok && tok < P.m, tok, n0 + j, (p0 + p1) + (p2 + p3));
+            }
+            return;
+        }
         // The tree: p_q = a_2q + a_2q+1 (PK = 2: across the lane halves),
         // then waves 1..3 hand their parts to wave 0.
         constexpr int NT = PK == 2 ? 1 : MT;
