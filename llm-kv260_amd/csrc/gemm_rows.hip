@@ -19,10 +19,9 @@
 // tokens' 512 activation bytes and 16 scales once for all its groups: one
 // barrier per segment, with the loads of the next segments in flight.
 //
-// The integer part is v_mfma_i32_16x16x32_i8 as in gemm_mfma.hip (K = 32 is
-// one block; unsigned nibbles, then a second MFMA against a constant -8
-// operand; at four token tiles the weights made signed once instead,
-// signed_nibbles). Operand layout of the 16x16x32 i8 MFMA (64 lanes):
+// The integer part is v_mfma_i32_16x16x32_i8 (K = 32 is one block), one MFMA
+// per block and token tile on the weights as 16 (n - 8) (block_weights).
+// Operand layout of the 16x16x32 i8 MFMA (64 lanes):
 //   A: lane l holds A[i = l % 16][k = 8 (l / 16) .. + 7]      (token i)
 //   B: lane l holds B[k = 8 (l / 16) .. + 7][j = l % 16]      (row j)
 //   D: lane l holds D[i = 4 (l / 16) + r][j = l % 16], r = 0..3
@@ -53,36 +52,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
 
 __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
-constexpr long MINUS8 = (long)0xF8F8F8F8F8F8F8F8ull;      // eight int8 -8s: the second MFMA's operand
-
 // DPP quad broadcast of lane R of each quad; folds into the consuming multiply.
 template <int R>
 __device__ __forceinline__ float bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), R * 0x55, 0xF, 0xF, true));
 }
 
-// Four nibble values n (one a byte, 0..15) as the signed bytes n - 8: n ^ 8
-// is n - 8 as a 4-bit two's-complement number, and its sign (bit 3) spread
-// over the byte's high nibble makes it the 8-bit one. The spread is a
-// multiply by 30 (8 * 30 = 240 = 0xF0) in two 16-bit halves, whose high
-// bytes never carry into each other.
-__device__ __forceinline__ uint32_t signed_nibbles(uint32_t n) {
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    const uint32_t x = n ^ 0x08080808u;
-    const uint32_t s = x & 0x08080808u;
-    const u16x2 r = __builtin_bit_cast(u16x2, s) * (u16x2){30, 30} + __builtin_bit_cast(u16x2, x);
-    return __builtin_bit_cast(uint32_t, r);
-}
-
 // Block B (0..15) of a staged segment, row j of the group: the MFMA weight
-// operand of lane group g (the nibbles of weights 8g .. 8g + 7: the low
-// nibbles of bytes 0..7, g = 0, and 8..15, g = 1, then the high nibbles,
-// g = 2, 3) and the block's scale. B's parity fixes where the scale and the
-// nibbles sit in their dwords.
+// operand of lane group g (weights 8g .. 8g + 7: the low nibbles of bytes
+// 0..7, g = 0, and 8..15, g = 1, then the high nibbles, g = 2, 3) and the
+// block's scale. The operand is 16 (n - 8) as signed bytes: each nibble n
+// moved to its byte's high half (where the high nibbles already are) and its
+// top bit flipped, (n << 4) ^ 0x80 = 16 (n - 8) as int8 -- as cheap as the
+// unsigned nibble, and it needs no second MFMA against -8. The MFMA sums are
+// then 16 sumi exactly, and the scale comes back as d_w / 16 (exact: a
+// power of two on an fp16 value, never subnormal in fp32), so the term
+// f32(16 sumi) * (d_w / 16) is the same product as f32(sumi) * d_w,
+// rounded once: every later operation sees the contract's value.
 template <int B>
-__device__ __forceinline__ void block_weights(const uint8_t *slab, int j, int g, long &bw, float &dw) {
+__device__ __forceinline__ void block_weights(const uint8_t *slab, int j, int g, long &bw, float &dw16) {
     const int h = g & 1;
-    const int shift = (g >> 1) * 4;
+    const int up = 4 - (g >> 1) * 4;            // 4: low nibbles, 0: high nibbles
     const uint8_t *wrow = slab + j * WPITCH + 18 * B;
     uint32_t lo, hi, d_bits;
     if constexpr ((B & 1) == 0) {
@@ -99,8 +89,8 @@ __device__ __forceinline__ void block_weights(const uint8_t *slab, int j, int g,
         hi = run[1];
         d_bits = *reinterpret_cast<const uint32_t *>(wrow - 2) >> 16;
     }
-    bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
-    dw = half_bits_to_float(d_bits);
+    bw = as_long(((lo << up) & 0xF0F0F0F0u) ^ 0x80808080u, ((hi << up) & 0xF0F0F0F0u) ^ 0x80808080u);
+    dw16 = half_bits_to_float(d_bits) * 0.0625f;
 }
 
 struct RowsParams {
@@ -244,10 +234,9 @@ __device__ __forceinline__ void store_y(const RowsParams &P, bool ok, int tok, i
 // only live outputs. The A operand's 16 rows are (block c, token t) =
 // (i / 4, i % 4); block c's MFMA sees zeros in every other block's rows, so
 // the four MFMAs put each block's exact int32 sums in its own rows of one
-// tile, and one more MFMA against -8 adds -8 sum(x) to every row. The
-// result's lane l then holds block c = l / 16 of the four, tokens r = 0..3,
-// row l % 16: every lane live, one fp32 term per value, and the lane's
-// accumulator is its block's.
+// tile. The result's lane l then holds block c = l / 16 of the four, tokens
+// r = 0..3, row l % 16: every lane live, one fp32 term per value, and the
+// lane's accumulator is its block's.
 struct PairKernel {
     static constexpr int GROUPS = 2;
     using G = Geo<1, GROUPS, 2>;
@@ -274,7 +263,6 @@ struct PairKernel {
         v4i d = {0, 0, 0, 0};
         float dw = 0.0f;
         packed_mfma<B0, 0>(slab, j, g, ablk, ax, d, dw);
-        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, MINUS8, d, 0, 0, 0);
         // The four tokens' scales of the lane's block: one 16-byte read (a
         // block's scales are a row of XDP floats, tokens along it).
         const float4 dx =
@@ -383,27 +371,12 @@ struct QuadKernel {
         block_weights<B>(slab, j, g, bw, dw);
         const uint8_t *xa = xq + j * G::APITCH + 32 * B + 8 * g;
         const float *xs = xd + B * G::XDP + 4 * g + (j & 3);
-        if constexpr (MT >= 4) {
-            // Four token tiles share the weight operand: make it the signed
-            // weights n - 8 once (three integer ops a dword) instead of a
-            // second MFMA per tile against -8.
-            const long sw = as_long(signed_nibbles((uint32_t)bw), signed_nibbles((uint32_t)((unsigned long)bw >> 32)));
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
-                dx[t] = xs[16 * t];
-                v4i z = {0, 0, 0, 0};
-                v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, sw, z, 0, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
-                dx[t] = xs[16 * t];
-                v4i z = {0, 0, 0, 0};
-                z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
-                v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, MINUS8, z, 0, 0, 0);
-            }
+        for (int t = 0; t < MT; ++t) {
+            const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::APITCH);
+            dx[t] = xs[16 * t];
+            v4i z = {0, 0, 0, 0};
+            v[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
         }
     }
 
@@ -456,7 +429,6 @@ struct QuadKernel {
         v4i d = {0, 0, 0, 0};
         d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ablk == 0 ? ax : 0L, bw0, d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ablk == 1 ? ax : 0L, bw1, d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, MINUS8, d, 0, 0, 0);
         const float dw = dblk == 0 ? dw0 : dw1;
         const float4 dx = *reinterpret_cast<const float4 *>(xd + (B0 + dblk) * G::XDP + dtok);
         const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
