@@ -6,9 +6,13 @@
 // MFMA: v_mfma_i32_16x16x32_i8 multiplies a 16 (tokens) x 32 by a 32 x 16
 // (rows) int8 tile. K = 32 is exactly one block, so each MFMA result is one
 // block's exact int32 sum for 16 x 16 (token, row) pairs, never mixed across
-// blocks. The weight operand is the unsigned nibble n (0..15); a second MFMA
-// against a constant -8 operand adds -8 * sum(x) into the same accumulator, so
-// the registers end up holding sum((n - 8) * x) with no VALU work.
+// blocks. The weight operand is 16 (n - 8) as a signed byte: each nibble n
+// moved to its byte's high half (the high nibbles are already there) and its
+// top bit flipped, (n << 4) ^ 0x80, two operations a dword like the unsigned
+// nibble's. The registers then hold 16 sum((n - 8) * x) exactly, and the
+// block's scale is taken as d_w / 16 (exact: a power of two on an fp16
+// value, never subnormal in fp32), so f32(16 sumi) * (d_w / 16) is the
+// contract's f32(sumi) * d_w, the same real product rounded once.
 //
 // Operand layout of the 16x16x32 i8 MFMA (64 lanes, 8 int8 per lane):
 //   A: lane l holds A[i = l % 16][k = 8 (l / 16) .. + 7]      (token i)
@@ -260,8 +264,7 @@ struct Kernel {
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
         const int j = lane & 15, g = lane >> 4;
         const int h = g & 1;
-        const int shift = (g >> 1) * 4;
-        const long minus8 = as_long(0xF8F8F8F8u, 0xF8F8F8F8u);
+        const int up = 4 - (g >> 1) * 4;         // 4: low nibbles, 0: high nibbles
         // Block 8c + w of row j starts at byte 18 w of its chunk: an even w at
         // a dword boundary (scale in the low half, the nibble run two bytes
         // in), an odd w two bytes into a dword (scale in the high half of the
@@ -293,15 +296,14 @@ struct Kernel {
                 hi = run[36 * c + 1];
                 d_bits = scl[36 * c] >> 16;
             }
-            const long bw = as_long((lo >> shift) & 0x0F0F0F0Fu, (hi >> shift) & 0x0F0F0F0Fu);
-            dw[c] = half_bits_to_float(d_bits);
+            const long bw = as_long(((lo << up) & 0xF0F0F0F0u) ^ 0x80808080u, ((hi << up) & 0xF0F0F0F0u) ^ 0x80808080u);
+            dw[c] = half_bits_to_float(d_bits) * 0.0625f;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const long ax = *reinterpret_cast<const long *>(xa + 16 * t * G::AP + 256 * c);
                 dx[c][t] = xs[8 * c * G::XDP + 16 * t];
                 v4i z = {0, 0, 0, 0};
-                z = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
-                v[c][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, minus8, z, 0, 0, 0);
+                v[c][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
             }
         }
         // Phase 2: the fp32 terms, added to each accumulator in block order.
