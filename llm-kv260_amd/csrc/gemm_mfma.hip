@@ -54,8 +54,8 @@
 // that runs on across its items.
 //
 // Matrices of 8,192 rows and more go to gemm_rows.hip instead, which cuts the
-// work along rows (a pair of waves per 16-row group for the whole of K): with
-// that many rows it fills the GPU without splitting K, and is faster.
+// work along rows (two or four waves per 16-row group for the whole of K):
+// with that many rows it fills the GPU without splitting K, and is faster.
 #include "kernels.h"
 #include "q4_0_device.h"
 
