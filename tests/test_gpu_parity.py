@@ -294,7 +294,12 @@ def test_gemv_quarters_at_separate_addresses(gpu):
                                       # and 4 blocks x 4 tokens (m <= 4 where the few-token GEMV does not
                                       # take the shape); ragged rows, 1-3 K segments
                                       (5, 8200, 2048), (8, 8256, 4096), (7, 9000, 1536), (6, 8192, 512),
-                                      (4, 8200, 12288), (2, 8193, 1024), (69, 8200, 1024)])
+                                      (4, 8200, 12288), (2, 8193, 1024), (69, 8200, 1024),
+                                      # the row-split quads on each side of their token tilings
+                                      # (8 | 9, 16 | 17, 32 | 33 tokens), ragged rows (not a whole
+                                      # workgroup of 32 or 64), 1-4 K segments
+                                      (9, 8200, 1024), (16, 8208, 2048), (17, 8200, 1536),
+                                      (32, 8200, 512), (33, 8240, 1024), (64, 8200, 2048)])
 def test_gemm_matches_rowwise_contract(gpu, m, rows, k):
     w = O.normal_f32((rows, k), 200 + m, 0.02)
     x = O.normal_f32((m, k), 300 + m)
