@@ -569,9 +569,8 @@ __global__ __launch_bounds__(64 * 4 * GROUPS) void gemm_rows_quad_kernel(RowsPar
 }
 
 template <class G>
-hipError_t launch_rows(const void *fn, void (*kernel)(RowsParams), const RowsParams &P, hipStream_t stream,
-                       int groups) {
-    const hipError_t e = allow_dynamic_lds(fn, LDS_MAX);
+hipError_t launch_rows(void (*kernel)(RowsParams), const RowsParams &P, hipStream_t stream, int groups) {
+    const hipError_t e = allow_dynamic_lds(reinterpret_cast<const void *>(kernel), LDS_MAX);
     if (e != hipSuccess) return e;
     const int grid = (P.rows + 16 * groups - 1) / (16 * groups);
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(G::THREADS), G::LDS, stream, P);
@@ -580,8 +579,8 @@ hipError_t launch_rows(const void *fn, void (*kernel)(RowsParams), const RowsPar
 
 template <int MT, int GROUPS, int PK = 1>
 hipError_t launch_rows_quad(const RowsParams &P, hipStream_t stream) {
-    auto *k = &gemm_rows_quad_kernel<MT, GROUPS, PK>;
-    return launch_rows<typename QuadKernel<MT, GROUPS, PK>::G>(reinterpret_cast<const void *>(k), k, P, stream, GROUPS);
+    return launch_rows<typename QuadKernel<MT, GROUPS, PK>::G>(&gemm_rows_quad_kernel<MT, GROUPS, PK>, P, stream,
+                                                               GROUPS);
 }
 
 }  // namespace
@@ -601,9 +600,7 @@ hipError_t launch_gemm_rows(const uint8_t *w, const uint8_t *x, int m, float *y,
     P.k = k;
     P.m = m;
     P.x_stride = k + k / 8;
-    if (m <= 4)
-        return launch_rows<PairKernel::G>(reinterpret_cast<const void *>(&gemm_rows_pair_kernel),
-                                          &gemm_rows_pair_kernel, P, stream, PairKernel::GROUPS);
+    if (m <= 4) return launch_rows<PairKernel::G>(&gemm_rows_pair_kernel, P, stream, PairKernel::GROUPS);
     // One token tile: two 16-row groups a workgroup, two workgroups a CU
     // (four groups a workgroup were slower: gate|up at 8 / 16 tokens 8.8
     // against 8.3 / 8.4 us, the LM head 48.2 / 51.7 against 43.6 / 49.5).
