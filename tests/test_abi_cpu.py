@@ -25,7 +25,8 @@ def _declared_functions() -> set[str]:
     for h in os.listdir(INCLUDE):
         if not h.endswith(".h"):
             continue
-        text = open(os.path.join(INCLUDE, h)).read()
+        with open(os.path.join(INCLUDE, h)) as f:
+            text = f.read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         text = re.sub(r"//[^\n]*", "", text)
         for m in re.finditer(r"^\s*(?!static|typedef|#)[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M):
